@@ -1,0 +1,289 @@
+// C ABI of libmvm_scan.so (declared in include/mvm_scan.h).
+//
+// Host-side responsibilities: validate every argument before anything is
+// enqueued, pick the time-chunk length, carve the caller's workspace into
+// the kernels' scratch buffers, and map HIP failures to MVM_ERR_HIP with a
+// thread-local message.  No device memory is allocated here.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "mvm_scan.h"
+#include "mvm_testing.h"
+#include "scan_common.h"
+#include "scan_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MVM_OK;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Channel-block workgroups per (b, k, chunk) and the time-chunk length.
+// Long sequences with few (batch x direction x channel) rows are cut into
+// chunks until the main passes launch >= 2048 waves (two per SIMD on the
+// 256-CU MI355X); every chunk is a whole number of 16-step tiles.
+int64_t pick_chunk_len(const mvm_scan_desc* d) {
+  if (d->chunk_len > 0) return d->chunk_len;
+  const int64_t tiles = ceil_div(d->seqlen, mvm::kSub);
+  const int64_t waves = d->batch * d->ndir * ceil_div(d->dim, mvm::kChPerBlock) * 4;
+  const int64_t target = 2048;
+  int64_t nchunk = waves >= target ? 1 : ceil_div(target, std::max<int64_t>(waves, 1));
+  // keep at least 4 tiles (64 positions) per chunk
+  nchunk = std::min(nchunk, std::max<int64_t>(1, tiles / 4));
+  const int64_t tiles_per_chunk = ceil_div(tiles, nchunk);
+  return std::max<int64_t>(1, tiles_per_chunk) * mvm::kSub;
+}
+
+int check_desc(const mvm_scan_desc* d) {
+  if (d == nullptr) return fail(MVM_ERR_INVALID_ARG, "desc is NULL");
+  if (d->batch < 0 || d->seqlen < 0 || d->dim < 0)
+    return fail(MVM_ERR_INVALID_ARG, "negative size (batch=%lld seqlen=%lld dim=%lld)",
+                (long long)d->batch, (long long)d->seqlen, (long long)d->dim);
+  if (d->dstate < 1 || d->dstate > MVM_MAX_DSTATE)
+    return fail(MVM_ERR_UNSUPPORTED, "dstate=%lld unsupported (1..%d)", (long long)d->dstate,
+                MVM_MAX_DSTATE);
+  if (d->ndir < 1) return fail(MVM_ERR_INVALID_ARG, "ndir=%lld must be >= 1", (long long)d->ndir);
+  if (d->in_dtype != MVM_F32 && d->in_dtype != MVM_BF16)
+    return fail(MVM_ERR_UNSUPPORTED, "in_dtype=%d unsupported", d->in_dtype);
+  if (d->out_dtype != MVM_F32 && d->out_dtype != MVM_BF16)
+    return fail(MVM_ERR_UNSUPPORTED, "out_dtype=%d unsupported", d->out_dtype);
+  if (d->chunk_len < 0 || d->chunk_len % mvm::kSub != 0)
+    return fail(MVM_ERR_INVALID_ARG, "chunk_len=%d must be 0 or a positive multiple of %d",
+                d->chunk_len, mvm::kSub);
+  const int64_t strides[6] = {d->x_stride_b, d->x_stride_k, d->x_stride_t,
+                              d->bc_stride_b, d->bc_stride_k, d->bc_stride_t};
+  for (int64_t s : strides)
+    if (s < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride");
+  if (d->seqlen > 1 && d->x_stride_t < d->dim)
+    return fail(MVM_ERR_INVALID_ARG, "x_stride_t=%lld overlaps channels (dim=%lld)",
+                (long long)d->x_stride_t, (long long)d->dim);
+  if (d->seqlen > 1 && d->bc_stride_t < d->dstate)
+    return fail(MVM_ERR_INVALID_ARG, "bc_stride_t=%lld overlaps states (dstate=%lld)",
+                (long long)d->bc_stride_t, (long long)d->dstate);
+  if (d->batch * d->ndir > 65535)
+    return fail(MVM_ERR_UNSUPPORTED, "batch*ndir=%lld exceeds 65535",
+                (long long)(d->batch * d->ndir));
+  if (d->seqlen > 0 && ceil_div(d->seqlen, pick_chunk_len(d)) > 65535)
+    return fail(MVM_ERR_UNSUPPORTED, "too many time chunks; raise chunk_len");
+  if (d->seqlen > INT32_MAX) return fail(MVM_ERR_UNSUPPORTED, "seqlen exceeds 2^31-1");
+  return MVM_OK;
+}
+
+mvm::Geom make_geom(const mvm_scan_desc* d) {
+  mvm::Geom g;
+  g.B = d->batch;
+  g.L = d->seqlen;
+  g.D = d->dim;
+  g.N = d->dstate;
+  g.K = d->ndir;
+  g.xsb = d->x_stride_b;
+  g.xsk = d->x_stride_k;
+  g.xst = d->x_stride_t;
+  g.bsb = d->bc_stride_b;
+  g.bsk = d->bc_stride_k;
+  g.bst = d->bc_stride_t;
+  g.tok = d->seq_to_tok;
+  g.chunk_len = pick_chunk_len(d);
+  g.nchunk = d->seqlen > 0 ? ceil_div(d->seqlen, g.chunk_len) : 0;
+  g.nsub = ceil_div(d->seqlen, mvm::kSub);
+  g.ncblk = ceil_div(d->dim, mvm::kChPerBlock);
+  return g;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace layouts (byte sizes; every piece 256-byte aligned).
+struct FwdWs {
+  size_t agg_h = 0, agg_s = 0, total = 0;
+};
+FwdWs fwd_ws(const mvm::Geom& g) {
+  FwdWs w;
+  if (g.nchunk > 1) {
+    const size_t slots = static_cast<size_t>(g.B * g.K * g.nchunk * g.D);
+    w.agg_h = align_up(slots * mvm::kStatePad * sizeof(float));
+    w.agg_s = align_up(slots * sizeof(float));
+  }
+  w.total = w.agg_h + w.agg_s;
+  return w;
+}
+
+struct BwdWs {
+  size_t agg_mu = 0, agg_s = 0, part_dA = 0, part_dD = 0, part_bc = 0, ckpt = 0, fwd = 0, total = 0;
+};
+BwdWs bwd_ws(const mvm::Geom& g, bool recompute_ckpt) {
+  BwdWs w;
+  const size_t slots = static_cast<size_t>(g.B * g.K * g.nchunk * g.D);
+  if (g.nchunk > 1) {
+    w.agg_mu = align_up(slots * mvm::kStatePad * sizeof(float));
+    w.agg_s = align_up(slots * sizeof(float));
+  }
+  w.part_dA = align_up(slots * mvm::kStatePad * sizeof(double));
+  w.part_dD = align_up(slots * sizeof(double));
+  w.part_bc = align_up(static_cast<size_t>(g.B * g.K * g.ncblk * g.L) * 2 * mvm::kStatePad * sizeof(float));
+  if (recompute_ckpt) {
+    w.ckpt = align_up(static_cast<size_t>(g.B * g.K * g.nsub * g.D) * mvm::kStatePad * sizeof(float));
+    w.fwd = fwd_ws(g).total;
+  }
+  w.total = w.agg_mu + w.agg_s + w.part_dA + w.part_dD + w.part_bc + w.ckpt + w.fwd;
+  return w;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MVM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvm_abi_version(void) { return MVM_ABI_VERSION; }
+
+const char* mvm_last_error(void) { return g_err; }
+
+int mvm_scan_validate(const mvm_scan_desc* desc) {
+  const int rc = check_desc(desc);
+  return rc == MVM_OK ? ok() : rc;
+}
+
+int64_t mvm_scan_ckpt_elems(const mvm_scan_desc* desc) {
+  const int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = make_geom(desc);
+  return g.B * g.K * g.nsub * g.D * mvm::kStatePad;
+}
+
+int64_t mvm_scan_workspace_bytes(const mvm_scan_desc* desc, int which) {
+  const int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = make_geom(desc);
+  if (which == 0) return static_cast<int64_t>(fwd_ws(g).total);
+  if (which == 1) return static_cast<int64_t>(bwd_ws(g, false).total);
+  if (which == 2) return static_cast<int64_t>(bwd_ws(g, true).total);
+  return fail(MVM_ERR_INVALID_ARG, "which=%d must be 0, 1 or 2", which);
+}
+
+int64_t mvm_scan_chunk_len(const mvm_scan_desc* desc) {
+  const int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  return make_geom(desc).chunk_len;
+}
+
+int mvm_scan_fwd(const mvm_scan_desc* desc, const void* u, const float* delta, const float* A,
+                 const void* Bm, const void* Cm, const float* Dv, void* y, float* ckpt,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = make_geom(desc);
+  const bool empty = g.B == 0 || g.L == 0 || g.D == 0;
+  if (!empty) {
+    if (!u || !delta || !A || !Bm || !Cm || !Dv)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fwd: NULL input pointer");
+    if (!y && !ckpt) return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fwd: y and ckpt are both NULL");
+    if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fwd: ckpt must be 16-byte aligned");
+  }
+  const FwdWs w = fwd_ws(g);
+  if (workspace_bytes < w.total)
+    return fail(MVM_ERR_WORKSPACE, "mvm_scan_fwd: workspace %zu bytes < %zu needed", workspace_bytes,
+                w.total);
+  if (w.total > 0 && workspace == nullptr)
+    return fail(MVM_ERR_WORKSPACE, "mvm_scan_fwd: workspace is NULL");
+  if ((reinterpret_cast<uintptr_t>(workspace) & (kAlign - 1)) != 0)
+    return fail(MVM_ERR_WORKSPACE, "mvm_scan_fwd: workspace must be %zu-byte aligned", kAlign);
+  if (empty) return ok();
+  char* ws = static_cast<char*>(workspace);
+  mvm::FwdBufs b{u, delta, A, Bm, Cm, Dv, y, ckpt,
+                 reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + w.agg_h)};
+  return hip_status(mvm::launch_fwd(g, b, desc->in_dtype, desc->out_dtype,
+                                    static_cast<hipStream_t>(stream)),
+                    "mvm_scan_fwd launch");
+}
+
+int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta, const float* A,
+                 const void* Bm, const void* Cm, const float* Dv, const float* ckpt,
+                 const void* dy, void* du, float* ddelta, float* dA, void* dB, void* dC,
+                 float* dD, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = make_geom(desc);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool empty = g.B == 0 || g.L == 0 || g.D == 0;
+  if (g.D > 0 && (!dA || !dD)) return fail(MVM_ERR_INVALID_ARG, "mvm_scan_bwd: NULL dA or dD");
+  if (!empty) {
+    if (!u || !delta || !A || !Bm || !Cm || !Dv || !dy)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_bwd: NULL input pointer");
+    if (!du || !ddelta || !dB || !dC)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_bwd: NULL output pointer");
+    if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_bwd: ckpt must be 16-byte aligned");
+  }
+  const bool recompute = ckpt == nullptr;
+  const BwdWs w = bwd_ws(g, recompute);
+  if (!empty) {
+    if (workspace_bytes < w.total)
+      return fail(MVM_ERR_WORKSPACE, "mvm_scan_bwd: workspace %zu bytes < %zu needed", workspace_bytes,
+                  w.total);
+    if (workspace == nullptr) return fail(MVM_ERR_WORKSPACE, "mvm_scan_bwd: workspace is NULL");
+    if ((reinterpret_cast<uintptr_t>(workspace) & (kAlign - 1)) != 0)
+      return fail(MVM_ERR_WORKSPACE, "mvm_scan_bwd: workspace must be %zu-byte aligned", kAlign);
+  }
+  if (empty) {
+    // sums over an empty (b, t) range are zero
+    hipError_t e = mvm::launch_fill(dA, g.K * g.D * g.N, 0.f, s);
+    if (e == hipSuccess) e = mvm::launch_fill(dD, g.K * g.D, 0.f, s);
+    return hip_status(e, "mvm_scan_bwd fill");
+  }
+  char* ws = static_cast<char*>(workspace);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    float* p = reinterpret_cast<float*>(ws + off);
+    off += bytes;
+    return bytes ? p : nullptr;
+  };
+  float* agg_mu = take(w.agg_mu);
+  float* agg_s = take(w.agg_s);
+  double* part_dA = reinterpret_cast<double*>(take(w.part_dA));
+  double* part_dD = reinterpret_cast<double*>(take(w.part_dD));
+  float* part_bc = take(w.part_bc);
+  float* ck = take(w.ckpt);
+  float* fws = take(w.fwd);
+  if (recompute) {
+    // the reference's VJP also recomputes the forward states
+    // (mamba_metal_fused.py:241-244); here only the 16-step checkpoints
+    const FwdWs fw = fwd_ws(g);
+    float* fagg_s = fws ? reinterpret_cast<float*>(reinterpret_cast<char*>(fws) + fw.agg_h) : nullptr;
+    mvm::FwdBufs fb{u, delta, A, Bm, Cm, Dv, nullptr, ck, fws, fagg_s};
+    hipError_t e = mvm::launch_fwd(g, fb, desc->in_dtype, desc->out_dtype, s);
+    if (e != hipSuccess) return hip_status(e, "mvm_scan_bwd checkpoint recompute");
+    ckpt = ck;
+  }
+  mvm::BwdBufs b{u, delta, A, Bm, Cm, Dv, ckpt, dy, du, ddelta, dA, dB, dC, dD,
+                 agg_mu, agg_s, part_dA, part_dD, part_bc};
+  return hip_status(mvm::launch_bwd(g, b, desc->in_dtype, desc->out_dtype, s), "mvm_scan_bwd launch");
+}
+
+int mvm_selftest_lanes(float* out, void* stream) {
+  if (out == nullptr) return fail(MVM_ERR_INVALID_ARG, "out is NULL");
+  return hip_status(mvm::launch_selftest_lanes(out, static_cast<hipStream_t>(stream)), "selftest");
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// Shared device-side helpers for the gfx950 selective-scan kernels.
+//
+// Lane layout used by every scan kernel (wave64):
+//   lane = 4 * c + g,  c = channel within the wave (0..15), g = state group
+//   (0..3).  Lane (c, g) holds states n = 4g .. 4g+3 of channel c in VGPRs,
+//   so a wave covers 16 channels x 16 states and a 256-thread workgroup
+//   covers 64 channels.  Sums over the 16 states of one channel are two DPP
+//   quad-permute adds; sums over the 16 channels of a wave use
+//   v_permlane32_swap / v_permlane16_swap (gfx950) and two DPP row rotates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvm {
+
+constexpr int kSub = 16;          // scan positions per tile == checkpoint interval
+constexpr int kThreads = 256;     // threads per workgroup (4 waves)
+constexpr int kChPerWave = 16;
+constexpr int kChPerBlock = 64;
+constexpr int kStatePad = 16;     // states per channel in every internal buffer
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+  // round to nearest even; NaN stays NaN (quiet bit forced)
+  uint32_t u = __float_as_uint(v);
+  bf16_t r;
+  if ((u & 0x7f800000u) == 0x7f800000u) {
+    r.bits = static_cast<uint16_t>((u >> 16) | ((u & 0x007fffffu) ? 0x0040u : 0u));
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.bits = static_cast<uint16_t>(u >> 16);
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
+template <typename T>
+__device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
+
+// Token row read / written at scan position t.  Table entries are clamped
+// to [0, L) so that a malformed remap table cannot address outside the
+// tensors (the clamp is scalar work on a wave-uniform value).
+__device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int64_t L) {
+  if (tok == nullptr) return t;
+  const int64_t r = tok[t];
+  return r < 0 ? 0 : (r >= L ? L - 1 : r);
+}
+
+// 2^x on the transcendental unit (v_exp_f32); callers pre-scale by log2(e).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------- DPP ops
+// dpp_ctrl encodings (GCN/CDNA): quad_perm = sel0 | sel1<<2 | sel2<<4 | sel3<<6,
+// row_ror:r = 0x120 + r.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kRowRor8 = 0x128;
+constexpr int kRowRor4 = 0x124;
+
+// Sum over the 4 lanes of a channel (lane bits 0-1); every lane gets the sum.
+__device__ __forceinline__ float sum_groups(float x) {
+  x += dpp<kQuadXor1>(x);
+  x += dpp<kQuadXor2>(x);
+  return x;
+}
+
+// v_permlane32_swap / v_permlane16_swap are issued through inline asm with
+// both registers as in/out operands: this toolchain's
+// __builtin_amdgcn_permlane{16,32}_swap keeps only element 0 of the
+// intrinsic's {vdst, vsrc} result and returns it for both halves.  The
+// leading s_nop 1 gives the two wait states a permlane needs after a VALU
+// write of its operands (the compiler inserts the same for the builtin).
+
+// v_permlane32_swap: lanes 32..63 of `a` trade places with lanes 0..31 of
+// `b`.  Afterwards a + b holds, in lanes 0..31, a summed over lanes (l, l+32)
+// and, in lanes 32..63, b summed over (l-32, l).
+__device__ __forceinline__ float pair_reduce32(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+// v_permlane16_swap: odd 16-lane rows of `a` trade places with even rows of
+// `b`.  Afterwards a + b holds, in rows 0 and 2, a summed over row pairs
+// (0,1) / (2,3) and, in rows 1 and 3, b summed over the same pairs.
+__device__ __forceinline__ float pair_reduce16(float a, float b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
+// Sum over the 16 channels of a wave of four per-lane values v[0..3] (the
+// lane's states 4g+j).  Returns, in lane (c, g) with j = (lane >> 4) & 3, the
+// channel sum of state 4g + j; lanes with equal (g, j) hold equal results.
+__device__ __forceinline__ float channel_reduce4(float v0, float v1, float v2, float v3) {
+  const float s02 = pair_reduce32(v0, v2);  // bit5=0 -> state j=0, bit5=1 -> j=2
+  const float s13 = pair_reduce32(v1, v3);  // bit5=0 -> j=1,        bit5=1 -> j=3
+  float s = pair_reduce16(s02, s13);        // row r=(bit5,bit4) -> j = r
+  s += dpp<kRowRor8>(s);                    // lane bit 3
+  s += dpp<kRowRor4>(s);                    // lane bit 2
+  return s;
+}
+
+}  // namespace mvm

@@ -1,0 +1,65 @@
+// Kernel parameter blocks and launch entry points shared by the scan
+// kernels (scan_fwd.hip, scan_bwd.hip) and the C ABI (capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvm {
+
+// Geometry of one scan call (all directions of one launch).
+struct Geom {
+  int64_t B, L, D, N, K;
+  int64_t xsb, xsk, xst;   // u-like strides
+  int64_t bsb, bsk, bst;   // B-like strides
+  const int32_t* tok;      // (K, L) scan position -> token row, or nullptr
+  int64_t chunk_len;       // multiple of kSub
+  int64_t nchunk;          // ceil(L / chunk_len)
+  int64_t nsub;            // ceil(L / kSub), checkpoint slots per (b, k, d)
+  int64_t ncblk;           // ceil(D / 64), channel blocks
+};
+
+struct FwdBufs {
+  const void* u;
+  const float* delta;
+  const float* A;
+  const void* Bm;
+  const void* Cm;
+  const float* Dv;
+  void* y;         // may be null
+  float* ckpt;     // may be null
+  float* agg_h;    // (B*K, nchunk, D, 16): chunk end states, then carry-ins
+  float* agg_s;    // (B*K, nchunk, D): sum of delta over each chunk
+};
+
+struct BwdBufs {
+  const void* u;
+  const float* delta;
+  const float* A;
+  const void* Bm;
+  const void* Cm;
+  const float* Dv;
+  const float* ckpt;
+  const void* dy;
+  void* du;
+  float* ddelta;
+  float* dA;
+  void* dB;
+  void* dC;
+  float* dD;
+  float* agg_mu;   // (B*K, nchunk, D, 16): adjoint aggregates, then carries
+  float* agg_s;    // (B*K, nchunk, D)
+  double* part_dA;  // (B*K, nchunk, D, 16) float64 partial sums
+  double* part_dD;  // (B*K, nchunk, D)
+  float* part_bc;  // (B*K, ncblk, L, 32): per channel-block dB | dC sums
+};
+
+// in_dtype / out_dtype follow MVM_F32 / MVM_BF16.
+hipError_t launch_fwd(const Geom& g, const FwdBufs& b, int in_dtype, int out_dtype,
+                      hipStream_t s);
+hipError_t launch_bwd(const Geom& g, const BwdBufs& b, int in_dtype, int out_dtype,
+                      hipStream_t s);
+hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t s);
+hipError_t launch_selftest_lanes(float* out, hipStream_t s);
+
+}  // namespace mvm

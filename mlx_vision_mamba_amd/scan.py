@@ -1,0 +1,288 @@
+"""Selective scan on MI355X: autograd Functions over the HIP C ABI.
+
+Drop-in for the reference's scan entry points (paths relative to the
+reference repository root):
+
+* ``selective_scan(x, delta, A, B, C, D) -> y``   mamba_block.py:20-74
+* ``selective_scan_chunked`` / ``selective_scan_parallel``   mamba_fast.py:17, :165
+* ``selective_scan_metal`` (forward only, no autograd)       mamba_metal.py:230
+* ``selective_scan_metal_trainable``                         mamba_metal.py:275
+* ``selective_scan_metal_fused``                             mamba_metal_fused.py:253
+
+All of them compute the same function with the same six gradients; they run
+the HIP kernels of libmvm_scan.so and differ only in how the sequence is cut
+into time chunks.  CPU tensors raise: there is no CPU fallback.
+
+``selective_scan_directions`` is the index-remapped multi-direction form
+used by the direction blocks: K scans over (B, L, K, D) token-order tensors,
+where scan position s of direction k reads and writes token row
+``seq_to_tok[k, s]`` (replacing the permuted copies of
+mamba_block.py:254-338, :443-533).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DT_CODE = {torch.float32: _lib.MVM_F32, torch.bfloat16: _lib.MVM_BF16}
+
+#: scan_mode names accepted by MambaBlock (mamba_block.py:104-122) plus "hip".
+SCAN_MODES = ("sequential", "chunked", "parallel", "metal", "metal_train", "metal_fused", "hip")
+
+
+def _stream_ptr(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _check_device(*ts):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "mlx_vision_mamba_amd scans run only on the GPU (HIP); got tensors on "
+            f"{dev}. There is no CPU fallback.")
+    for t in ts:
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"all scan tensors must be on {dev}; got one on {t.device}")
+
+
+def _make_desc(u, Bm, in_dt, out_dt, tok, chunk_len):
+    bsz, L, K, D = u.shape
+    N = Bm.shape[-1]
+    d = _lib.ScanDesc()
+    d.batch, d.seqlen, d.dim, d.dstate, d.ndir = bsz, L, D, N, K
+    d.x_stride_b, d.x_stride_t, d.x_stride_k = u.stride(0), u.stride(1), u.stride(2)
+    d.bc_stride_b, d.bc_stride_t, d.bc_stride_k = Bm.stride(0), Bm.stride(1), Bm.stride(2)
+    d.seq_to_tok = tok.data_ptr() if tok is not None else None
+    d.in_dtype = _DT_CODE[in_dt]
+    d.out_dtype = _DT_CODE[out_dt]
+    d.chunk_len = int(chunk_len)
+    return d
+
+
+def _resolve_chunk(L, chunk_len):
+    """chunk_len: int >= 0 (0 = library heuristic) or 'whole' (one chunk)."""
+    if chunk_len == "whole":
+        return max(16, (L + 15) // 16 * 16)
+    return int(chunk_len)
+
+
+def _prepare(u, delta, A, Bm, Cm, Dv):
+    """Canonicalise dtypes / layouts; shapes are (B,L,K,D), (K,D,N), (B,L,K,N), (K,D)."""
+    if u.dim() != 4 or delta.shape != u.shape:
+        raise ValueError(f"u and delta must be (B, L, K, D) of equal shape; got {tuple(u.shape)}, "
+                         f"{tuple(delta.shape)}")
+    bsz, L, K, D = u.shape
+    if A.dim() != 3 or A.shape[0] != K or A.shape[1] != D:
+        raise ValueError(f"A must be (K={K}, D={D}, N); got {tuple(A.shape)}")
+    N = A.shape[2]
+    if N < 1 or N > _lib.MVM_MAX_DSTATE:
+        raise ValueError(f"d_state={N} unsupported (1..{_lib.MVM_MAX_DSTATE})")
+    if Bm.shape != (bsz, L, K, N) or Cm.shape != (bsz, L, K, N):
+        raise ValueError(f"B and C must be {(bsz, L, K, N)}; got {tuple(Bm.shape)}, {tuple(Cm.shape)}")
+    if Dv.shape != (K, D):
+        raise ValueError(f"D must be {(K, D)}; got {tuple(Dv.shape)}")
+    _check_device(u, delta, A, Bm, Cm, Dv)
+    in_dt = torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in (u, Bm, Cm)) else torch.float32
+    u = u.to(in_dt).contiguous()
+    Bm = Bm.to(in_dt)
+    Cm = Cm.to(in_dt)
+    if not (Bm.stride() == Cm.stride() and Bm.stride(-1) == 1 and min(Bm.stride()) >= 0):
+        Bm, Cm = Bm.contiguous(), Cm.contiguous()
+    delta = delta.to(torch.float32).contiguous()
+    A = A.to(torch.float32).contiguous()
+    Dv = Dv.to(torch.float32).contiguous()
+    return u, delta, A, Bm, Cm, Dv, in_dt
+
+
+def scan_forward(u, delta, A, Bm, Cm, Dv, tok=None, chunk_len=0, out_dtype=None, save_ckpt=False):
+    """Raw forward launch (no autograd).  Returns (y, ckpt or None).
+
+    Shapes: u, delta (B,L,K,D); A (K,D,N); Bm, Cm (B,L,K,N); Dv (K,D);
+    tok (K,L) int32 on the same device or None.
+    """
+    u, delta, A, Bm, Cm, Dv, in_dt = _prepare(u, delta, A, Bm, Cm, Dv)
+    out_dt = out_dtype or in_dt
+    L = u.shape[1]
+    desc = _make_desc(u, Bm, in_dt, out_dt, tok, _resolve_chunk(L, chunk_len))
+    lib = _lib.lib()
+    dev = u.device
+    with torch.cuda.device(dev):
+        y = torch.empty(u.shape, dtype=out_dt, device=dev)
+        ckpt = None
+        if save_ckpt:
+            ckpt = torch.empty(_lib.check(lib.mvm_scan_ckpt_elems(ctypes.byref(desc))),
+                               dtype=torch.float32, device=dev)
+        nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), 0))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.mvm_scan_fwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
+                                    _ptr(Cm), _ptr(Dv), _ptr(y), _ptr(ckpt), _ptr(ws), nbytes,
+                                    ctypes.c_void_p(_stream_ptr(dev))))
+    return y, ckpt
+
+
+def scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt=None, tok=None, chunk_len=0, out_dtype=None):
+    """Raw VJP launch.  Returns float32/out-dtype (du, ddelta, dA, dB, dC, dD)."""
+    u, delta, A, Bm, Cm, Dv, in_dt = _prepare(u, delta, A, Bm, Cm, Dv)
+    out_dt = out_dtype or in_dt
+    L = u.shape[1]
+    desc = _make_desc(u, Bm, in_dt, out_dt, tok, _resolve_chunk(L, chunk_len))
+    lib = _lib.lib()
+    dev = u.device
+    dy = dy.to(in_dt).contiguous()
+    if dy.shape != u.shape:
+        raise ValueError(f"dy shape {tuple(dy.shape)} != {tuple(u.shape)}")
+    with torch.cuda.device(dev):
+        du = torch.empty(u.shape, dtype=out_dt, device=dev)
+        ddelta = torch.empty(u.shape, dtype=torch.float32, device=dev)
+        dA = torch.empty(A.shape, dtype=torch.float32, device=dev)
+        dB = torch.empty_strided(Bm.shape, Bm.stride(), dtype=out_dt, device=dev)
+        dC = torch.empty_strided(Bm.shape, Bm.stride(), dtype=out_dt, device=dev)
+        dD = torch.empty(Dv.shape, dtype=torch.float32, device=dev)
+        which = 1 if ckpt is not None else 2
+        nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), which))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.mvm_scan_bwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
+                                    _ptr(Cm), _ptr(Dv), _ptr(ckpt), _ptr(dy), _ptr(du),
+                                    _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD),
+                                    _ptr(ws), nbytes, ctypes.c_void_p(_stream_ptr(dev))))
+    return du, ddelta, dA, dB, dC, dD
+
+
+class _SelectiveScanFn(torch.autograd.Function):
+    """y = scan(u, delta, A, B, C, D) with the fused HIP VJP
+    (the custom_function + vjp pair of mamba_metal_fused.py:229-250)."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, Bm, Cm, Dv, tok, chunk_len, out_dtype):
+        needs = any(ctx.needs_input_grad[:6])
+        y, ckpt = scan_forward(u, delta, A, Bm, Cm, Dv, tok, chunk_len, out_dtype, save_ckpt=needs)
+        ctx.chunk_len = chunk_len
+        ctx.out_dtype = out_dtype
+        ctx.in_dtypes = tuple(t.dtype for t in (u, delta, A, Bm, Cm, Dv))
+        if needs:
+            ctx.save_for_backward(u, delta, A, Bm, Cm, Dv, ckpt, tok)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        u, delta, A, Bm, Cm, Dv, ckpt, tok = ctx.saved_tensors
+        grads = scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt, tok, ctx.chunk_len, ctx.out_dtype)
+        grads = tuple(g.to(dt) for g, dt in zip(grads, ctx.in_dtypes))
+        return grads + (None, None, None)
+
+
+def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0, out_dtype=None):
+    """K index-remapped scans in one launch.
+
+    u, delta: (B, L, K, D) in token order; A: (K, D, N); B, C: (B, L, K, N);
+    D: (K, D); seq_to_tok: (K, L) int32 tensor on the GPU (or None for the
+    identity order).  Returns y (B, L, K, D) in token order.
+    """
+    if seq_to_tok is not None:
+        if seq_to_tok.dtype != torch.int32 or seq_to_tok.shape != (u.shape[2], u.shape[1]):
+            raise ValueError("seq_to_tok must be int32 of shape (K, L)")
+        seq_to_tok = seq_to_tok.to(u.device).contiguous()
+    return _SelectiveScanFn.apply(u, delta, A, B, C, D, seq_to_tok, chunk_len, out_dtype)
+
+
+def _scan3(x, delta, A, B, C, D, chunk_len, out_dtype=None):
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D); got {tuple(x.shape)}")
+    y = _SelectiveScanFn.apply(x.unsqueeze(2), delta.unsqueeze(2), A.unsqueeze(0), B.unsqueeze(2),
+                               C.unsqueeze(2), D.unsqueeze(0), None, chunk_len, out_dtype)
+    return y.squeeze(2)
+
+
+def selective_scan(x, delta, A, B, C, D, chunk_len=0, out_dtype=None):
+    """Selective scan (S6), forward + VJP on the GPU.  mamba_block.py:20-74.
+
+    x, delta: (B, L, D_inner); A: (D_inner, N); B, C: (B, L, N); D: (D_inner,).
+    ``chunk_len`` = 0 lets the library cut long sequences into time chunks
+    (two-pass carry); ``"whole"`` keeps one chunk per channel.
+    """
+    return _scan3(x, delta, A, B, C, D, chunk_len, out_dtype)
+
+
+def selective_scan_sequential(x, delta, A, B, C, D):
+    """Sequential in time: one chunk per channel (the ``sequential`` mode)."""
+    return _scan3(x, delta, A, B, C, D, "whole")
+
+
+def selective_scan_chunked(x, delta, A, B, C, D, chunk_size=32):
+    """mamba_fast.py:17 ``chunked`` mode: time chunks of ``chunk_size``
+    (rounded up to a multiple of 16) joined by the carry pass."""
+    return _scan3(x, delta, A, B, C, D, max(16, (int(chunk_size) + 15) // 16 * 16))
+
+
+def selective_scan_parallel(x, delta, A, B, C, D):
+    """mamba_fast.py:165 ``parallel`` mode: chunk-parallel scan, chunk
+    length chosen by the library."""
+    return _scan3(x, delta, A, B, C, D, 0)
+
+
+def selective_scan_metal(x, delta, A, B, C, D):
+    """mamba_metal.py:230 ``metal`` mode: inference only, no autograd (the
+    result is detached and no checkpoints are written)."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, D); got {tuple(x.shape)}")
+    y, _ = scan_forward(x.detach().unsqueeze(2), delta.detach().unsqueeze(2), A.detach().unsqueeze(0),
+                        B.detach().unsqueeze(2), C.detach().unsqueeze(2), D.detach().unsqueeze(0))
+    return y.squeeze(2)
+
+
+def selective_scan_metal_trainable(x, delta, A, B, C, D):
+    """mamba_metal.py:275 ``metal_train`` mode (same function and gradients)."""
+    return _scan3(x, delta, A, B, C, D, 0)
+
+
+def selective_scan_metal_fused(x, delta, A, B, C, D):
+    """mamba_metal_fused.py:253 ``metal_fused`` mode."""
+    return _scan3(x, delta, A, B, C, D, 0)
+
+
+_MODE_FNS = {
+    "sequential": selective_scan_sequential,
+    "chunked": selective_scan_chunked,
+    "parallel": selective_scan_parallel,
+    "metal": selective_scan_metal,
+    "metal_train": selective_scan_metal_trainable,
+    "metal_fused": selective_scan_metal_fused,
+    "hip": selective_scan,
+}
+
+# chunk_len used by the direction blocks for each mode
+_MODE_CHUNK = {"sequential": "whole", "chunked": 32, "parallel": 0, "metal": 0,
+               "metal_train": 0, "metal_fused": 0, "hip": 0}
+
+
+def get_scan_fn(scan_mode: str):
+    """Scan function for a scan_mode string (mamba_block.py:104-122).
+
+    Unknown names raise ValueError (the reference silently fell back to the
+    sequential scan, mamba_block.py:121-122).
+    """
+    try:
+        return _MODE_FNS[scan_mode]
+    except KeyError:
+        raise ValueError(f"unknown scan_mode {scan_mode!r}; expected one of {SCAN_MODES}") from None
+
+
+def mode_chunk_len(scan_mode: str):
+    get_scan_fn(scan_mode)
+    return _MODE_CHUNK[scan_mode]
+
+
+def selftest_lanes(device="cuda"):
+    """Runs the cross-lane layout check kernel; returns a (128,) float tensor."""
+    out = torch.empty(128, dtype=torch.float32, device=device)
+    with torch.cuda.device(out.device):
+        _lib.check(_lib.lib().mvm_selftest_lanes(_ptr(out), ctypes.c_void_p(_stream_ptr(out.device))))
+    return out

@@ -1,0 +1,99 @@
+"""ctypes binding of the float64 C oracle (oracle/scan_ref.c).
+
+TEST INFRASTRUCTURE ONLY -- see oracle/__init__.py.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "liboracle_scan.so")
+_lib = None
+
+
+def build():
+    """Compile scan_ref.c with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            build()
+        lib = ctypes.CDLL(_SO)
+        i64, fp, dp = ctypes.c_int64, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double)
+        lib.oracle_scan_fwd.argtypes = [i64] * 4 + [fp] * 6 + [dp]
+        lib.oracle_scan_fwd.restype = ctypes.c_int
+        lib.oracle_scan_vjp.argtypes = [i64] * 4 + [fp] * 7 + [dp] * 6
+        lib.oracle_scan_vjp.restype = ctypes.c_int
+        lib.oracle_ddelta_scale.argtypes = [i64] * 4 + [fp] * 6 + [dp]
+        lib.oracle_ddelta_scale.restype = ctypes.c_int
+        lib.oracle_num_threads.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def _f32(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _p(a, ct):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def num_threads() -> int:
+    return int(_load().oracle_num_threads())
+
+
+def scan_fwd(u, delta, A, B, C, D):
+    """float64 y for float32 inputs (B,L,D),(B,L,D),(D,N),(B,L,N),(B,L,N),(D,)."""
+    lib = _load()
+    u, delta, A, B, C, D = map(_f32, (u, delta, A, B, C, D))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    y = np.empty((bsz, L, d), dtype=np.float64)
+    fp = ctypes.c_float
+    rc = lib.oracle_scan_fwd(bsz, L, d, n, _p(u, fp), _p(delta, fp), _p(A, fp),
+                             _p(B, fp), _p(C, fp), _p(D, fp), _p(y, ctypes.c_double))
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_fwd failed ({rc})")
+    return y
+
+
+def scan_vjp(u, delta, A, B, C, D, g):
+    """float64 (du, ddelta, dA, dB, dC, dD)."""
+    lib = _load()
+    u, delta, A, B, C, D, g = map(_f32, (u, delta, A, B, C, D, g))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    outs = [np.empty((bsz, L, d)), np.empty((bsz, L, d)), np.empty((d, n)),
+            np.empty((bsz, L, n)), np.empty((bsz, L, n)), np.empty((d,))]
+    fp, dp = ctypes.c_float, ctypes.c_double
+    rc = lib.oracle_scan_vjp(bsz, L, d, n, _p(u, fp), _p(delta, fp), _p(A, fp),
+                             _p(B, fp), _p(C, fp), _p(D, fp), _p(g, fp),
+                             *[_p(o, dp) for o in outs])
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_vjp failed ({rc})")
+    return tuple(outs)
+
+
+def ddelta_scale(u, delta, A, B, C, g):
+    """float64 S[b,t,d] = sum_n |lam_n| (|A_n e_n h_{t-1,n}| + |B_n u_t|):
+    the cancellation scale of ddelta (see scan_ref.c)."""
+    lib = _load()
+    u, delta, A, B, C, g = map(_f32, (u, delta, A, B, C, g))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    out = np.empty((bsz, L, d), dtype=np.float64)
+    fp = ctypes.c_float
+    rc = lib.oracle_ddelta_scale(bsz, L, d, n, _p(u, fp), _p(delta, fp), _p(A, fp), _p(B, fp),
+                                 _p(C, fp), _p(g, fp), _p(out, ctypes.c_double))
+    if rc != 0:
+        raise RuntimeError(f"oracle_ddelta_scale failed ({rc})")
+    return out

@@ -1,0 +1,201 @@
+/*
+ * Float64 C restatement of the reference's selective scan -- TEST
+ * INFRASTRUCTURE ONLY (the oracle).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's CPU-baseline leg load this library.
+ *
+ * Same algorithm as oracle/scan_oracle.py (which is pinned by closed forms,
+ * autograd and finite differences in tests/test_oracle.py), restated in C so
+ * that parity checks at full sequence lengths finish in seconds:
+ *
+ *   forward   mamba_block.py:45-74: h_t = exp(delta_t*A) h_{t-1}
+ *             + delta_t*B_t*u_t ; y_t = sum_n C_t h_t + D*u_t
+ *   VJP       mamba_metal_fused.py:66-145 (adjoint lam += C*g, per-step
+ *             grads from lam and h_{t-1}, lam *= exp(delta*A)) and the
+ *             reductions at :213-224 (dD over b, dA over b and t, dB and dC
+ *             over channels).
+ *
+ * Inputs are float32 (the exact values handed to the GPU), all arithmetic
+ * and outputs are float64.  Channels are independent, so the loops run one
+ * (b, d) pair at a time and keep only that pair's L x N states.
+ * tests/test_oracle.py checks this library against scan_oracle.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* y: (B, L, D) float64. */
+int oracle_scan_fwd(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                    const float* u, const float* delta, const float* A,
+                    const float* Bm, const float* Cm, const float* Dv,
+                    double* y) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < Bsz; ++b) {
+    for (int64_t d = 0; d < D; ++d) {
+      double h[64];
+      for (int64_t n = 0; n < N; ++n) h[n] = 0.0;
+      for (int64_t t = 0; t < L; ++t) {
+        const int64_t xi = (b * L + t) * D + d;
+        const int64_t bi = (b * L + t) * N;
+        const double dt = delta[xi], x = u[xi];
+        double acc = 0.0;
+        for (int64_t n = 0; n < N; ++n) {
+          const double e = exp(dt * (double)A[d * N + n]);
+          h[n] = e * h[n] + dt * (double)Bm[bi + n] * x;
+          acc += h[n] * (double)Cm[bi + n];
+        }
+        y[xi] = acc + x * (double)Dv[d];
+      }
+    }
+  }
+  return 0;
+}
+
+/* Reverse-scan VJP.  du, ddelta: (B,L,D); dA: (D,N); dB, dC: (B,L,N);
+ * dD: (D).  All float64, fully reduced. */
+int oracle_scan_vjp(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                    const float* u, const float* delta, const float* A,
+                    const float* Bm, const float* Cm, const float* Dv,
+                    const float* g, double* du, double* ddelta, double* dA,
+                    double* dB, double* dC, double* dD) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+  const int64_t nbl = Bsz * L * N;
+  memset(dA, 0, sizeof(double) * (size_t)(D * N));
+  memset(dB, 0, sizeof(double) * (size_t)nbl);
+  memset(dC, 0, sizeof(double) * (size_t)nbl);
+  memset(dD, 0, sizeof(double) * (size_t)D);
+  int fail = 0;
+#pragma omp parallel
+  {
+    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    double* lB = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lC = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lA = (double*)calloc((size_t)(D * N), sizeof(double));
+    double* lD = (double*)calloc((size_t)D, sizeof(double));
+    const int ok = hs && lB && lC && lA && lD;
+    if (!ok) {
+#pragma omp atomic write
+      fail = 1;
+    }
+    /* every thread reaches the worksharing loop; one without buffers idles */
+#pragma omp for collapse(2) schedule(static)
+      for (int64_t b = 0; b < Bsz; ++b) {
+        for (int64_t d = 0; d < D; ++d) {
+          if (!ok) continue;
+          /* hs[(t+1)*N + n] = h_t, hs[0..N) = h_{-1} = 0 */
+          for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;
+          for (int64_t t = 0; t < L; ++t) {
+            const int64_t xi = (b * L + t) * D + d;
+            const int64_t bi = (b * L + t) * N;
+            const double dt = delta[xi], x = u[xi];
+            for (int64_t n = 0; n < N; ++n) {
+              const double e = exp(dt * (double)A[d * N + n]);
+              hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x;
+            }
+          }
+          double lam[64];
+          for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;
+          double dDacc = 0.0;
+          for (int64_t t = L - 1; t >= 0; --t) {
+            const int64_t xi = (b * L + t) * D + d;
+            const int64_t bi = (b * L + t) * N;
+            const double dt = delta[xi], x = u[xi], gy = g[xi];
+            dDacc += gy * x;
+            double sdu = 0.0, sdd = 0.0;
+            for (int64_t n = 0; n < N; ++n) {
+              const double a = A[d * N + n];
+              const double e = exp(dt * a);
+              const double bv = Bm[bi + n];
+              const double hp = hs[t * N + n];
+              lam[n] += (double)Cm[bi + n] * gy;
+              sdd += lam[n] * (hp * a * e + bv * x);
+              lA[d * N + n] += lam[n] * hp * dt * e;
+              lB[bi + n] += lam[n] * dt * x;
+              lC[bi + n] += gy * hs[(t + 1) * N + n];
+              sdu += lam[n] * dt * bv;
+              lam[n] *= e;
+            }
+            du[xi] = gy * (double)Dv[d] + sdu;
+            ddelta[xi] = sdd;
+          }
+          lD[d] += dDacc;
+        }
+      }
+#pragma omp critical
+      if (ok) {
+        for (int64_t i = 0; i < nbl; ++i) { dB[i] += lB[i]; dC[i] += lC[i]; }
+        for (int64_t i = 0; i < D * N; ++i) dA[i] += lA[i];
+        for (int64_t i = 0; i < D; ++i) dD[i] += lD[i];
+      }
+    free(hs); free(lB); free(lC); free(lA); free(lD);
+  }
+  return fail ? -2 : 0;
+}
+
+/* Cancellation scale of ddelta: S[b,t,d] = sum_n |lam_n| * (|A_n e_n h_{t-1,n}|
+ * + |B_n u_t|), the sum of the absolute values of the terms whose signed sum
+ * is ddelta (same adjoint recurrence as oracle_scan_vjp).  An fp32
+ * evaluation of ddelta cannot be closer than about 2^-24 * S to the exact
+ * value, so the GPU parity test widens its bound by a multiple of S. */
+int oracle_ddelta_scale(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                        const float* u, const float* delta, const float* A,
+                        const float* Bm, const float* Cm, const float* g,
+                        double* scale) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+  int fail = 0;
+#pragma omp parallel
+  {
+    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    const int ok = hs != NULL;
+    if (!ok) {
+#pragma omp atomic write
+      fail = 1;
+    }
+#pragma omp for collapse(2) schedule(static)
+    for (int64_t b = 0; b < Bsz; ++b) {
+      for (int64_t d = 0; d < D; ++d) {
+        if (!ok) continue;
+        for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;
+        for (int64_t t = 0; t < L; ++t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi];
+          for (int64_t n = 0; n < N; ++n) {
+            const double e = exp(dt * (double)A[d * N + n]);
+            hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x;
+          }
+        }
+        double lam[64];
+        for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;
+        for (int64_t t = L - 1; t >= 0; --t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi], gy = g[xi];
+          double s = 0.0;
+          for (int64_t n = 0; n < N; ++n) {
+            const double a = A[d * N + n];
+            const double e = exp(dt * a);
+            lam[n] += (double)Cm[bi + n] * gy;
+            s += fabs(lam[n]) * (fabs(a * e * hs[t * N + n]) + fabs((double)Bm[bi + n] * x));
+            lam[n] *= e;
+          }
+          scale[xi] = s;
+        }
+      }
+    }
+    free(hs);
+  }
+  return fail ? -2 : 0;
+}

@@ -1,0 +1,155 @@
+"""Host-side checks of the C ABI (no GPU needed, no kernel launches).
+
+The library must load on a machine without a GPU, export every entry point
+its headers declare, and reject bad arguments on the host -- before anything
+is enqueued -- with the documented error codes.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from mlx_vision_mamba_amd import _lib, scan
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = []
+    for hdr in ("mvm_scan.h", "mvm_testing.h"):
+        text = open(os.path.join(ROOT, "include", hdr)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _declared_functions()
+    assert "mvm_scan_fwd" in declared and "mvm_scan_bwd" in declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.SIGNATURES)
+    assert lib.mvm_abi_version() == _lib.ABI_VERSION
+
+
+def _header_arity():
+    """Parameter count of every function declared in the headers."""
+    out = {}
+    for hdr in ("mvm_scan.h", "mvm_testing.h"):
+        text = open(os.path.join(ROOT, "include", hdr)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for name, params in re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+            params = params.strip()
+            out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_header_arity():
+    arity = _header_arity()
+    assert set(arity) == set(_lib.SIGNATURES)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == arity[name], name
+
+
+def _desc(B=2, L=40, D=24, N=16, K=1):
+    d = _lib.ScanDesc()
+    d.batch, d.seqlen, d.dim, d.dstate, d.ndir = B, L, D, N, K
+    d.x_stride_b, d.x_stride_t, d.x_stride_k = L * K * D, K * D, D
+    d.bc_stride_b, d.bc_stride_t, d.bc_stride_k = L * K * N, K * N, N
+    return d
+
+
+def _validate(d):
+    return _lib.lib().mvm_scan_validate(ctypes.byref(d))
+
+
+def test_valid_desc_and_sizes():
+    d = _desc()
+    assert _validate(d) == 0
+    lib = _lib.lib()
+    assert lib.mvm_scan_ckpt_elems(ctypes.byref(d)) == 2 * 1 * 3 * 24 * 16   # ceil(40/16)=3
+    assert lib.mvm_scan_chunk_len(ctypes.byref(d)) % 16 == 0
+    for which in (0, 1, 2):
+        assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), which) >= 0
+    assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), 7) == _lib.MVM_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dstate", 17, _lib.MVM_ERR_UNSUPPORTED),      # the reference's float h[16] cap
+    ("dstate", 0, _lib.MVM_ERR_UNSUPPORTED),
+    ("batch", -1, _lib.MVM_ERR_INVALID_ARG),
+    ("seqlen", -3, _lib.MVM_ERR_INVALID_ARG),
+    ("ndir", 0, _lib.MVM_ERR_INVALID_ARG),
+    ("in_dtype", 7, _lib.MVM_ERR_UNSUPPORTED),
+    ("out_dtype", 2, _lib.MVM_ERR_UNSUPPORTED),
+    ("chunk_len", 24, _lib.MVM_ERR_INVALID_ARG),
+    ("x_stride_t", 3, _lib.MVM_ERR_INVALID_ARG),
+    ("bc_stride_t", 2, _lib.MVM_ERR_INVALID_ARG),
+    ("x_stride_b", -5, _lib.MVM_ERR_INVALID_ARG),
+])
+def test_bad_descriptors_rejected(field, value, code):
+    d = _desc()
+    setattr(d, field, value)
+    assert _validate(d) == code
+    assert _lib.last_error() != ""
+
+
+def test_null_pointers_rejected_before_launch():
+    lib = _lib.lib()
+    d = _desc()
+    null = ctypes.c_void_p(0)
+    rc = lib.mvm_scan_fwd(ctypes.byref(d), *([null] * 9), 0, null)
+    assert rc == _lib.MVM_ERR_INVALID_ARG
+    assert "NULL" in _lib.last_error()
+    rc = lib.mvm_scan_bwd(ctypes.byref(d), *([null] * 15), 0, null)
+    assert rc == _lib.MVM_ERR_INVALID_ARG
+
+
+def test_small_workspace_rejected_before_launch():
+    lib = _lib.lib()
+    d = _desc(L=4096, D=64)
+    need = lib.mvm_scan_workspace_bytes(ctypes.byref(d), 1)
+    assert need > 0
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+    rc = lib.mvm_scan_bwd(ctypes.byref(d), *([fake] * 15), need - 1, ctypes.c_void_p(0))
+    assert rc == _lib.MVM_ERR_WORKSPACE
+    assert "workspace" in _lib.last_error()
+
+
+def test_null_desc():
+    assert _lib.lib().mvm_scan_validate(None) == _lib.MVM_ERR_INVALID_ARG
+
+
+def test_auto_chunking_fills_the_chip_for_long_sequences():
+    lib = _lib.lib()
+    d = _desc(B=8, L=16384, D=1536)
+    cl = lib.mvm_scan_chunk_len(ctypes.byref(d))
+    nchunk = -(-16384 // cl)
+    waves = 8 * 24 * 4 * nchunk
+    assert cl % 16 == 0 and waves >= 2048
+    d2 = _desc(B=32, L=196, D=768, K=4)
+    assert lib.mvm_scan_chunk_len(ctypes.byref(d2)) >= 196   # enough rows: one chunk
+
+
+def test_cpu_tensors_raise_no_fallback():
+    x = torch.randn(1, 8, 4)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        scan.selective_scan(x, x.abs(), -torch.ones(4, 16), torch.randn(1, 8, 16),
+                            torch.randn(1, 8, 16), torch.ones(4))
+
+
+def test_scan_mode_registry():
+    for m in scan.SCAN_MODES:
+        assert callable(scan.get_scan_fn(m))
+    with pytest.raises(ValueError, match="unknown scan_mode"):
+        scan.get_scan_fn("metal_fast")
+
+
+def test_shape_errors():
+    with pytest.raises(ValueError):
+        scan.scan_forward(torch.zeros(1, 2, 1, 3), torch.zeros(1, 2, 1, 3), torch.zeros(1, 3, 17),
+                          torch.zeros(1, 2, 1, 17), torch.zeros(1, 2, 1, 17), torch.zeros(1, 3))

@@ -1,0 +1,212 @@
+"""Pins the oracle (oracle/scan_oracle.py, oracle/scan_ref.c, oracle/torch_ref.py).
+
+Each check comes from something other than the oracle's own formula: closed
+forms, a textbook library routine (numpy cumsum, scipy lfilter), a scalar
+brute-force loop, torch autograd of an independent forward, and finite
+differences (gradcheck).  A dropped term, a wrong sign, an off-by-one in time
+or a transposed operand in the oracle fails at least one of these.
+"""
+
+import numpy as np
+import pytest
+import scipy.signal
+import torch
+
+from oracle import ref_lib, scan_oracle as so, torch_ref
+from tests import scan_inputs
+
+
+def _rand(bsz, L, D, N, seed=0, a_mode="s4d"):
+    u, dl, A, Bm, Cm, Dv, g = scan_inputs.make(bsz, L, D, N, seed=seed, a_mode=a_mode)
+    return [t.double().numpy() for t in (u, dl, A, Bm, Cm, Dv, g)]
+
+
+# ----------------------------------------------------------------- forward
+
+def test_closed_form_single_step():
+    u, dl, A, Bm, Cm, Dv, _ = _rand(3, 1, 7, 16, seed=1)
+    Dv = np.linspace(0.5, 2.0, 7)
+    y = so.scan_fwd(u, dl, A, Bm, Cm, Dv)
+    # h_0 = delta*B*u  =>  y = u*(D + delta*sum_n B_n C_n)
+    expect = u * (Dv + dl * np.sum(Bm * Cm, axis=-1)[..., None])
+    np.testing.assert_allclose(y, expect, rtol=1e-13, atol=1e-13)
+
+
+def test_closed_form_zero_decay_is_cumsum():
+    u, dl, _, Bm, Cm, Dv, _ = _rand(2, 23, 5, 4, seed=2)
+    A = np.zeros((5, 4))
+    y = so.scan_fwd(u, dl, A, Bm, Cm, Dv)
+    h = np.cumsum(dl[..., None] * Bm[:, :, None, :] * u[..., None], axis=1)
+    expect = np.einsum("bldn,bln->bld", h, Cm) + u * Dv
+    np.testing.assert_allclose(y, expect, rtol=1e-12, atol=1e-12)
+
+
+def test_closed_form_constant_decay_is_lfilter():
+    rng = np.random.default_rng(3)
+    L = 40
+    u = rng.standard_normal((1, L, 1))
+    dl = np.full((1, L, 1), 0.07)
+    A = np.array([[-2.5]])
+    Bm = rng.standard_normal((1, L, 1))
+    Cm = np.ones((1, L, 1))
+    y = so.scan_fwd(u, dl, A, Bm, Cm, np.zeros(1))
+    a = np.exp(0.07 * -2.5)
+    b = (dl * Bm * u)[0, :, 0]
+    expect = scipy.signal.lfilter([1.0], [1.0, -a], b)
+    np.testing.assert_allclose(y[0, :, 0], expect, rtol=1e-12, atol=1e-14)
+
+
+def test_zero_delta_and_zero_projections_give_skip_only():
+    u, dl, A, Bm, Cm, Dv, _ = _rand(2, 9, 6, 16, seed=4)
+    Dv = np.arange(6) * 0.3 - 0.7
+    for args in [(u, np.zeros_like(dl), A, Bm, Cm, Dv),
+                 (u, dl, A, np.zeros_like(Bm), Cm, Dv),
+                 (u, dl, A, Bm, np.zeros_like(Cm), Dv)]:
+        np.testing.assert_allclose(so.scan_fwd(*args), u * Dv, atol=1e-15)
+
+
+def test_linear_in_u():
+    u, dl, A, Bm, Cm, Dv, _ = _rand(2, 17, 4, 8, seed=5)
+    u2 = _rand(2, 17, 4, 8, seed=6)[0]
+    y = so.scan_fwd(2.0 * u - 3.0 * u2, dl, A, Bm, Cm, Dv)
+    expect = 2.0 * so.scan_fwd(u, dl, A, Bm, Cm, Dv) - 3.0 * so.scan_fwd(u2, dl, A, Bm, Cm, Dv)
+    np.testing.assert_allclose(y, expect, rtol=1e-12, atol=1e-12)
+
+
+def _brute_force(u, dl, A, Bm, Cm, Dv):
+    bsz, L, D = u.shape
+    N = A.shape[1]
+    y = np.zeros((bsz, L, D))
+    for b in range(bsz):
+        for d in range(D):
+            h = [0.0] * N
+            for t in range(L):
+                acc = 0.0
+                for n in range(N):
+                    h[n] = np.exp(dl[b, t, d] * A[d, n]) * h[n] + dl[b, t, d] * Bm[b, t, n] * u[b, t, d]
+                    acc += h[n] * Cm[b, t, n]
+                y[b, t, d] = acc + Dv[d] * u[b, t, d]
+    return y
+
+
+def test_brute_force_loop():
+    args = _rand(2, 6, 3, 5, seed=7, a_mode="random")
+    np.testing.assert_allclose(so.scan_fwd(*args[:6]), _brute_force(*args[:6]), rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 32, 40])
+def test_chunked_and_two_pass_equal_sequential(chunk):
+    args = _rand(2, 37, 5, 16, seed=8)[:6]
+    y = so.scan_fwd(*args)
+    np.testing.assert_allclose(so.scan_fwd_chunked(*args, chunk_size=chunk), y, rtol=0, atol=0)
+    np.testing.assert_allclose(so.scan_fwd_two_pass(*args, chunk_len=chunk), y, rtol=1e-12, atol=1e-13)
+
+
+def test_combine_is_associative():
+    rng = np.random.default_rng(9)
+    p = [(rng.uniform(0.1, 1, 16), rng.standard_normal(16)) for _ in range(3)]
+    left = so.combine(so.combine(p[0], p[1]), p[2])
+    right = so.combine(p[0], so.combine(p[1], p[2]))
+    np.testing.assert_allclose(left[0], right[0], rtol=1e-14)
+    np.testing.assert_allclose(left[1], right[1], rtol=1e-13)
+    # applying the combined pair equals applying the steps one by one
+    h0 = rng.standard_normal(16)
+    h = h0
+    for a, b in p:
+        h = a * h + b
+    np.testing.assert_allclose(left[0] * h0 + left[1], h, rtol=1e-13)
+
+
+# --------------------------------------------------------------------- VJP
+
+def _autograd_vjp(args, g):
+    ts = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in args]
+    y = torch_ref.scan_sequential(*ts)
+    grads = torch.autograd.grad(y, ts, torch.tensor(g))
+    return [x.numpy() for x in grads]
+
+
+@pytest.mark.parametrize("shape,a_mode", [((2, 13, 4, 16), "s4d"), ((1, 9, 3, 5), "random"),
+                                          ((3, 1, 2, 16), "s4d")])
+def test_vjp_matches_autograd(shape, a_mode):
+    *args, g = _rand(*shape, seed=10, a_mode=a_mode)
+    ours = so.scan_vjp(*args, g)
+    ref = _autograd_vjp(args, g)
+    for name, a, b in zip(["du", "ddelta", "dA", "dB", "dC", "dD"], ours, ref):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12, err_msg=name)
+
+
+def test_torch_restatement_gradcheck():
+    *args, _ = _rand(1, 5, 2, 3, seed=11, a_mode="random")
+    # scale delta up so exp(delta*A) differs visibly from 1
+    args[1] = args[1] * 20
+    ts = tuple(torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in args)
+    assert torch.autograd.gradcheck(torch_ref.scan_sequential, ts, eps=1e-6, atol=1e-7)
+    tc = tuple(torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in args)
+    assert torch.autograd.gradcheck(lambda *x: torch_ref.scan_chunked(*x, chunk_size=2), tc,
+                                    eps=1e-6, atol=1e-7)
+
+
+def test_vjp_closed_forms():
+    *args, g = _rand(2, 11, 3, 4, seed=12)
+    du, ddelta, dA, dB, dC, dD = so.scan_vjp(*args, g)
+    u = args[0]
+    np.testing.assert_allclose(dD, np.sum(g * u, axis=(0, 1)), rtol=1e-13)
+    # delta = 0: no state, lam_t = sum_{s>=t} C_s g_s, ddelta_t = sum_n lam B u
+    zero = [args[0], np.zeros_like(args[1])] + args[2:]
+    _, ddelta0, dA0, dB0, dC0, _ = so.scan_vjp(*zero, g)
+    Bm, Cm = args[3], args[4]
+    lam = np.flip(np.cumsum(np.flip(Cm[:, :, None, :] * g[..., None], 1), 1), 1)
+    expect = np.sum(lam * Bm[:, :, None, :], axis=-1) * u
+    np.testing.assert_allclose(ddelta0, expect, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(dA0, 0.0, atol=1e-15)
+    np.testing.assert_allclose(dB0, 0.0, atol=1e-15)
+    np.testing.assert_allclose(dC0, 0.0, atol=1e-15)
+
+
+# ------------------------------------------------------------- C restatement
+
+@pytest.mark.parametrize("shape,a_mode", [((2, 37, 5, 16), "s4d"), ((1, 50, 3, 7), "random"),
+                                          ((2, 1, 4, 16), "s4d")])
+def test_c_oracle_matches_numpy(shape, a_mode):
+    *args, g = _rand(*shape, seed=13, a_mode=a_mode)
+    f32 = [a.astype(np.float32) for a in args + [g]]
+    np.testing.assert_allclose(ref_lib.scan_fwd(*f32[:6]), so.scan_fwd(*f32[:6]), rtol=1e-12, atol=1e-13)
+    for a, b in zip(ref_lib.scan_vjp(*f32), so.scan_vjp(*f32[:6], f32[6])):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+def test_c_oracle_rejects_bad_state_size():
+    *args, g = _rand(1, 3, 2, 4, seed=14)
+    bad = [a.astype(np.float32) for a in args]
+    bad[2] = np.zeros((2, 65), np.float32)
+    with pytest.raises(RuntimeError):
+        ref_lib.scan_fwd(*bad)
+
+
+# ------------------------------------------------------------ direction remap
+
+@pytest.mark.parametrize("K,grid", [(2, (7, 3)), (4, (5, 3)), (6, (2, 3, 4)), (8, (2, 3, 2, 2))])
+def test_seq_to_token_matches_materialised_permutation(K, grid):
+    """The index table equals what the reference's reshape/transpose/flip
+    does to a token axis (mamba_block.py:254-338, :443-533)."""
+    n = int(np.prod(grid))
+    tokens = torch.arange(n, dtype=torch.float64).reshape(1, n, 1)
+    for k in range(K):
+        axes, rev = so.direction_axis_order(K, k)
+        seq = tokens if axes is None else torch_ref._permute(tokens, grid, axes)
+        if rev:
+            seq = seq.flip(1)
+        table = so.seq_to_token(n, grid, axes, rev)
+        np.testing.assert_array_equal(seq[0, :, 0].numpy().astype(np.int64), table)
+        # the inverse restores token order
+        if axes is not None:
+            back = torch_ref._unpermute(seq.flip(1) if rev else seq, grid, axes)
+            np.testing.assert_array_equal(back[0, :, 0].numpy(), np.arange(n))
+
+
+def test_direction_labels_follow_outermost_axis():
+    """K=6 pair 1 uses axis order (1,0,2): the innermost (fastest) axis is
+    still Z, as in mamba_block.py:478-482."""
+    table = so.seq_to_token(24, (2, 3, 4), (1, 0, 2), False)
+    assert list(table[:5]) == [0, 1, 2, 3, 12]
