@@ -1,0 +1,213 @@
+"""Benchmark: VisionMamba-2D K=4 train step on one MI355X, plus the selective
+scan's fwd+VJP bandwidth, printed as one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload (the step timed): VisionMamba encoder, 2D, K=4 scan directions,
+batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
+384 (d_inner 768), d_state 16, depth 6, float32 random-init weights
+(Kaiming-uniform projections, S4D-real A, dt bias with softplus(bias) in
+[1e-3, 1e-1]); loss = mean of the output features; one step = forward +
+loss + backward + AdamW update.  Inputs are resident on the GPU before the
+timed region; W untimed warm-up steps, then exactly K steps between two
+device synchronisations.  value = images / second.
+
+roofline: the selective-scan backward call (the largest hand-written piece
+of the step; its kernels are listed in "kernel"), timed with HIP events on
+the stream it runs on for every launch inside the timed region; achieved =
+algorithmic bytes per launch / mean launch time, against the MI355X HBM3E
+peak of 8 TB/s.
+
+scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
+D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads.
+
+cpu_baseline: the oracle's CPU restatement of the reference's sequential
+VisionMamba step (materialised discretisation, Python time loop, autograd)
+on this host's cores, on a bounded sample (batch 2, one step).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "selective-scan fwd+VJP GB/s & % HBM peak; VisionMamba-2D train imgs/sec"
+HBM_PEAK_GBS = 8000.0
+BWD_KERNELS = "mvm_scan_bwd: scan_bwd_agg_kernel + scan_bwd_carry_kernel + scan_bwd_kernel + reduce_bc_kernel + reduce_ad_kernel"
+
+
+def _seeded_model(torch, mvm, device):
+    torch.manual_seed(1001)
+    model = mvm.VisionMamba(img_size=224, patch_size=16, in_channels=1, embed_dim=384, depth=6,
+                            d_state=16, input_dim=2, scan_mode="hip")
+    return model.to(device)
+
+
+def bench_step(torch, mvm, scan, steps, warmup, device):
+    model = _seeded_model(torch, mvm, device)
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(32, 224, 224, 1, generator=gen).to(device)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = model(x).mean()
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    records = []
+    scan.set_scan_timing(records)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    scan.set_scan_timing(None)
+    if not math.isfinite(float(loss)):
+        raise RuntimeError("non-finite loss")
+    per = {"fwd": [], "bwd": []}
+    for kind, e0, e1, nbytes in records:
+        per[kind].append((e0.elapsed_time(e1) * 1e-3, nbytes))
+    return elapsed, per
+
+
+def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
+    from tests import scan_inputs
+    u, dl, A, Bm, Cm, Dv, g = [t.to(device) for t in scan_inputs.make(bsz, L, D, N, seed=0,
+                                                                         dtype=dtype)]
+    args = (u.unsqueeze(2), dl.unsqueeze(2), A.unsqueeze(0), Bm.unsqueeze(2), Cm.unsqueeze(2),
+            Dv.unsqueeze(0))
+    g4 = g.unsqueeze(2)
+    for _ in range(3):
+        y, ck = scan.scan_forward(*args, save_ckpt=True)
+        scan.scan_backward(*args, g4, ckpt=ck)
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    tf = tb = 0.0
+    for _ in range(iters):
+        evs[0].record()
+        y, ck = scan.scan_forward(*args, save_ckpt=True)
+        evs[1].record()
+        scan.scan_backward(*args, g4, ckpt=ck)
+        evs[2].record()
+        torch.cuda.synchronize()
+        tf += evs[0].elapsed_time(evs[1]) * 1e-3
+        tb += evs[1].elapsed_time(evs[2]) * 1e-3
+    tf /= iters
+    tb /= iters
+    size = 2 if dtype == torch.bfloat16 else 4
+    bf, bb = scan.algorithmic_bytes(bsz, L, D, N, size, size)
+    total = tf + tb
+    return {
+        "shape": f"B={bsz} L={L} D={D} N={N} {'bf16' if size == 2 else 'fp32'}",
+        "fwd_us": round(tf * 1e6, 2), "vjp_us": round(tb * 1e6, 2),
+        "algorithmic_bytes": bf + bb,
+        "GBps": round((bf + bb) / total / 1e9, 1),
+        "pct_hbm_peak": round((bf + bb) / total / 1e9 / HBM_PEAK_GBS * 100, 2),
+        "tokens_per_s": round(bsz * L / total, 1),
+    }
+
+
+def cpu_baseline(torch):
+    """Oracle VisionMamba step on the host cores: batch 2, one step."""
+    from oracle import torch_ref
+    import mlx_vision_mamba_amd as mvm
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(1001)
+    model = mvm.VisionMamba(img_size=224, patch_size=16, in_channels=1, embed_dim=384, depth=6,
+                            d_state=16, input_dim=2)
+    params = {k: v.detach().clone().requires_grad_(True) for k, v in model.named_parameters()}
+    x = torch.randn(2, 224, 224, 1, generator=torch.Generator().manual_seed(1))
+
+    def step():
+        for p in params.values():
+            p.grad = None
+        out = torch_ref.vision_mamba(params, x, input_dim=2, patch_size=16, depth=6,
+                                     grid_shape=(14, 14), d_state=16, d_conv=4)
+        out.mean().backward()
+
+    step()  # warm-up
+    t0 = time.perf_counter()
+    step()
+    dt = time.perf_counter() - t0
+    return {"value": round(2 / dt, 3), "unit": "imgs/s", "cores": cores, "kind": "port",
+            "sample": "VisionMamba-2D K=4 step (fwd + mean loss + bwd), batch 2 of the same "
+                      "224x224x1 / patch 16 / E=384 / depth 6 model, float32, reference's "
+                      "sequential scan restated in torch; 1 warm-up + 1 timed step",
+            "seconds_per_step": round(dt, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the selective-scan path is benchmarked on a "
+              "single MI355X (see DESIGN.md for how it would shard); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mlx_vision_mamba_amd as mvm
+    from mlx_vision_mamba_amd import scan
+
+    device = torch.device("cuda:0")
+    elapsed, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
+    imgs = 32 * args.steps / elapsed
+
+    bwd = per["bwd"]
+    bwd_t = sum(t for t, _ in bwd) / len(bwd)
+    bwd_b = sum(b for _, b in bwd) / len(bwd)
+    fwd = per["fwd"]
+    fwd_t = sum(t for t, _ in fwd) / len(fwd)
+    fwd_b = sum(b for _, b in fwd) / len(fwd)
+    achieved = bwd_b / bwd_t / 1e9
+    roofline = {
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "kernel": BWD_KERNELS,
+        "algorithmic_bytes_per_launch": int(bwd_b), "avg_launch_us": round(bwd_t * 1e6, 2),
+        "launches": len(bwd),
+        "fwd_call": {"achieved": round(fwd_b / fwd_t / 1e9, 1), "avg_launch_us": round(fwd_t * 1e6, 2),
+                     "algorithmic_bytes_per_launch": int(fwd_b)},
+    }
+    scans = {
+        "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 50, device),
+        "long_B8_L16384_bf16": bench_scan(torch, scan, 8, 16384, 1536, 16, torch.bfloat16, 5, device),
+    }
+    out = {
+        "metric": METRIC, "value": round(imgs, 2), "unit": "imgs/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) images, random-init weights)",
+        "config": {"workload": "VisionMamba-2D K=4 train step (fwd + mean loss + bwd + AdamW)",
+                   "global_batch": 32, "image": "224x224x1", "patch": 16, "seq_len": 196,
+                   "embed_dim": 384, "d_inner": 768, "d_state": 16, "depth": 6,
+                   "directions": 4, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "scan": scans,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

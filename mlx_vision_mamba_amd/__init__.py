@@ -20,4 +20,33 @@ from .scan import (  # noqa: F401
     selective_scan_sequential,
 )
 
+from .mamba_block import (  # noqa: F401
+    BidirectionalMambaBlock,
+    MambaBlock,
+    MultiDirectionalMambaBlock,
+    ResidualMambaBlock,
+)
+from .vision_mamba import PatchEmbed4D, VisionMamba  # noqa: F401
+from .vit import PatchEmbed, PatchEmbed3D  # noqa: F401
+
 __version__ = "0.1.0"
+__all__ = [
+    "MambaBlock",
+    "BidirectionalMambaBlock",
+    "MultiDirectionalMambaBlock",
+    "ResidualMambaBlock",
+    "VisionMamba",
+    "PatchEmbed",
+    "PatchEmbed3D",
+    "PatchEmbed4D",
+    "selective_scan",
+    "selective_scan_chunked",
+    "selective_scan_parallel",
+    "selective_scan_sequential",
+    "selective_scan_directions",
+    "selective_scan_metal",
+    "selective_scan_metal_trainable",
+    "selective_scan_metal_fused",
+    "SCAN_MODES",
+    "get_scan_fn",
+]

@@ -34,6 +34,39 @@ _DT_CODE = {torch.float32: _lib.MVM_F32, torch.bfloat16: _lib.MVM_BF16}
 SCAN_MODES = ("sequential", "chunked", "parallel", "metal", "metal_train", "metal_fused", "hip")
 
 
+# Optional per-call timing: when a list, every forward / backward launch
+# appends (kind, start_event, end_event, algorithmic_bytes), the events being
+# recorded on the stream the kernels run on.
+_timing = None
+
+
+def set_scan_timing(records):
+    """Start (pass a list) or stop (pass None) recording scan launches."""
+    global _timing
+    _timing = records
+
+
+def algorithmic_bytes(bsz, L, D, N, in_size, out_size, ndir=1):
+    """Bytes a scan forward / VJP must move if every tensor is read or
+    written exactly once: (forward, vjp).  delta, ddelta, A, dA, D, dD are
+    float32; u, B, C, dy use in_size and y, du, dB, dC use out_size bytes.
+    ``bsz`` counts (batch, direction) rows; A and D exist once per direction."""
+    fwd = (bsz * L * D * (in_size + 4 + out_size) + bsz * L * N * 2 * in_size
+           + ndir * (D * N * 4 + D * 4))
+    vjp = (bsz * L * D * (in_size + 4 + in_size + out_size + 4)
+           + bsz * L * N * (2 * in_size + 2 * out_size) + ndir * (D * N * 8 + D * 8))
+    return fwd, vjp
+
+
+def _record(kind, u, Bm, in_dt, out_dt):
+    bsz, L, K, D = u.shape
+    fwd, vjp = algorithmic_bytes(bsz * K, L, D, Bm.shape[-1], _SIZE[in_dt], _SIZE[out_dt], K)
+    return fwd if kind == "fwd" else vjp
+
+
+_SIZE = {torch.float32: 4, torch.bfloat16: 2}
+
+
 def _stream_ptr(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -122,9 +155,15 @@ def scan_forward(u, delta, A, Bm, Cm, Dv, tok=None, chunk_len=0, out_dtype=None,
                                dtype=torch.float32, device=dev)
         nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), 0))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        if _timing is not None:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
         _lib.check(lib.mvm_scan_fwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
                                     _ptr(Cm), _ptr(Dv), _ptr(y), _ptr(ckpt), _ptr(ws), nbytes,
                                     ctypes.c_void_p(_stream_ptr(dev))))
+        if _timing is not None:
+            ev1.record()
+            _timing.append(("fwd", ev0, ev1, _record("fwd", u, Bm, in_dt, out_dt)))
     return y, ckpt
 
 
@@ -149,10 +188,16 @@ def scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt=None, tok=None, chunk_len=0,
         which = 1 if ckpt is not None else 2
         nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), which))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        if _timing is not None:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
         _lib.check(lib.mvm_scan_bwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
                                     _ptr(Cm), _ptr(Dv), _ptr(ckpt), _ptr(dy), _ptr(du),
                                     _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD),
                                     _ptr(ws), nbytes, ctypes.c_void_p(_stream_ptr(dev))))
+        if _timing is not None:
+            ev1.record()
+            _timing.append(("bwd", ev0, ev1, _record("bwd", u, Bm, in_dt, out_dt)))
     return du, ddelta, dA, dB, dC, dD
 
 
@@ -179,17 +224,24 @@ class _SelectiveScanFn(torch.autograd.Function):
         return grads + (None, None, None)
 
 
-def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0, out_dtype=None):
+def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0, out_dtype=None,
+                              forward_only=False):
     """K index-remapped scans in one launch.
 
     u, delta: (B, L, K, D) in token order; A: (K, D, N); B, C: (B, L, K, N);
     D: (K, D); seq_to_tok: (K, L) int32 tensor on the GPU (or None for the
     identity order).  Returns y (B, L, K, D) in token order.
+    ``forward_only`` returns a detached y without saving checkpoints (the
+    reference's inference-only ``metal`` mode).
     """
     if seq_to_tok is not None:
         if seq_to_tok.dtype != torch.int32 or seq_to_tok.shape != (u.shape[2], u.shape[1]):
             raise ValueError("seq_to_tok must be int32 of shape (K, L)")
         seq_to_tok = seq_to_tok.to(u.device).contiguous()
+    if forward_only:
+        y, _ = scan_forward(u.detach(), delta.detach(), A.detach(), B.detach(), C.detach(),
+                            D.detach(), seq_to_tok, _resolve_chunk(u.shape[1], chunk_len), out_dtype)
+        return y
     return _SelectiveScanFn.apply(u, delta, A, B, C, D, seq_to_tok, chunk_len, out_dtype)
 
 

@@ -1,0 +1,107 @@
+"""Host-side checks of the module layer (no scan launches)."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mlx_vision_mamba_amd import directions as dirs
+from mlx_vision_mamba_amd import mamba_block as mb
+from mlx_vision_mamba_amd import vision_mamba as vm
+from mlx_vision_mamba_amd import vit
+from oracle import scan_oracle as so
+from oracle import torch_ref
+
+
+@pytest.mark.parametrize("K,grid", [(2, None), (4, (14, 14)), (4, (3, 5)), (6, (4, 3, 5)),
+                                    (8, (2, 3, 2, 4))])
+def test_tables_match_oracle(K, grid):
+    n = int(np.prod(grid)) if grid else 11
+    table = dirs.seq_to_tok_table(K, n, grid)
+    for k in range(K):
+        axes, rev = so.direction_axis_order(K, k)
+        np.testing.assert_array_equal(table[k].numpy(), so.seq_to_token(n, grid, axes, rev))
+    inv = dirs.inverse_table(table)
+    for k in range(K):
+        np.testing.assert_array_equal(table[k][inv[k].long()].numpy(), np.arange(n))
+
+
+@pytest.mark.parametrize("K,grid", [(2, None), (4, (3, 4)), (6, (2, 3, 2)), (8, (2, 1, 3, 2))])
+def test_remapped_causal_conv_matches_materialised_permutation(K, grid):
+    torch.manual_seed(0)
+    n = int(np.prod(grid)) if grid else 9
+    bsz, din, kc = 2, 5, 4
+    xb = torch.randn(bsz, n, K, din, dtype=torch.float64)
+    w = torch.randn(K * din, 1, kc, dtype=torch.float64)
+    b = torch.randn(K * din, dtype=torch.float64)
+    tok = dirs.seq_to_tok_table(K, n, grid)
+    got = mb._causal_conv(xb, tok, w, b, kc)
+    for k in range(K):
+        axes, rev = so.direction_axis_order(K, k)
+        seq = xb[:, :, k, :]
+        if axes is not None:
+            seq = torch_ref._permute(seq, grid, axes)
+        if rev:
+            seq = seq.flip(1)
+        out = F.conv1d(seq.transpose(1, 2), w[k * din:(k + 1) * din], b[k * din:(k + 1) * din],
+                       padding=kc - 1, groups=din)[..., :n].transpose(1, 2)
+        if rev:
+            out = out.flip(1)
+        if axes is not None:
+            out = torch_ref._unpermute(out, grid, axes)
+        torch.testing.assert_close(got[:, :, k, :], out, rtol=1e-12, atol=1e-12)
+
+
+def test_patch_embeds_equal_strided_convolution():
+    torch.manual_seed(1)
+    pe = vit.PatchEmbed(3, 8, 4).double()
+    x = torch.randn(2, 16, 12, 3, dtype=torch.float64)
+    ref = F.conv2d(x.permute(0, 3, 1, 2), pe.proj.weight, pe.proj.bias, stride=4)
+    torch.testing.assert_close(pe(x), ref.flatten(2).transpose(1, 2))
+    pe3 = vit.PatchEmbed3D(2, 8, 4).double()
+    x3 = torch.randn(2, 8, 12, 4, 2, dtype=torch.float64)
+    ref3 = F.conv3d(x3.permute(0, 4, 1, 2, 3), pe3.proj.weight, pe3.proj.bias, stride=4)
+    torch.testing.assert_close(pe3(x3), ref3.flatten(2).transpose(1, 2))
+    pe4 = vm.PatchEmbed4D(1, 8, 4, temporal_patch_size=2).double()
+    x4 = torch.randn(2, 4, 8, 8, 4, 1, dtype=torch.float64)
+    params = {"patch_embed.proj.weight": pe4.proj.weight, "patch_embed.proj.bias": pe4.proj.bias,
+              "pos_embed": torch.zeros(1, 2 * 2 * 2 * 1, 8, dtype=torch.float64),
+              "norm.weight": torch.ones(8, dtype=torch.float64),
+              "norm.bias": torch.zeros(8, dtype=torch.float64)}
+    ref4 = torch_ref.vision_mamba(params, x4, input_dim=4, patch_size=4, depth=0,
+                                  grid_shape=(2, 2, 2, 1), d_state=16, d_conv=4,
+                                  temporal_patch_size=2)
+    got4 = F.layer_norm(pe4(x4), (8,), params["norm.weight"], params["norm.bias"], 1e-5)
+    torch.testing.assert_close(got4, ref4)
+
+
+def test_constructor_errors():
+    with pytest.raises(ValueError):
+        mb.MultiDirectionalMambaBlock(32, num_directions=3)
+    with pytest.raises(ValueError):
+        mb.MultiDirectionalMambaBlock(32, num_directions=4, grid_shape=None)
+    with pytest.raises(ValueError):
+        mb.MultiDirectionalMambaBlock(32, num_directions=6, grid_shape=(2, 2))
+    with pytest.raises(ValueError):
+        mb.MambaBlock(32, scan_mode="not_a_mode")
+    with pytest.raises(ValueError):
+        vm.VisionMamba(img_size=32, patch_size=16, embed_dim=16, depth=1, input_dim=5)
+
+
+def test_scan_mode_passed_down():
+    v = vm.VisionMamba(img_size=32, patch_size=16, embed_dim=16, depth=2, scan_mode="chunked")
+    modes = {m.scan_mode for m in v.modules() if isinstance(m, mb.MambaBlock)}
+    assert modes == {"chunked"}
+
+
+def test_parameter_names_and_init():
+    blk = mb.MambaBlock(d_model=48, d_state=16)
+    names = dict(blk.named_parameters())
+    assert names["in_proj.weight"].shape == (192, 48)
+    assert names["conv1d.weight"].shape == (96, 1, 4)
+    assert names["x_proj.weight"].shape == (3 + 32, 96)      # dt_rank = ceil(48/16) = 3
+    assert names["dt_proj.weight"].shape == (96, 3)
+    assert names["out_proj.weight"].shape == (48, 96)
+    torch.testing.assert_close(-torch.exp(blk.A_log[0]), -torch.arange(1, 17, dtype=torch.float32))
+    dt = F.softplus(blk.dt_proj.bias)
+    assert float(dt.min()) >= 1e-3 * (1 - 1e-5) and float(dt.max()) <= 1e-1 * (1 + 1e-5)
