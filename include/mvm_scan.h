@@ -97,8 +97,8 @@ const char* mvm_last_error(void);
 int mvm_scan_validate(const mvm_scan_desc* desc);
 
 /* Number of float32 elements of the state checkpoint buffer the forward
- * writes for the backward: states after every 16th scan position,
- * (batch*ndir, ceil(seqlen/16), dim, 16).  Returns < 0 on a bad desc. */
+ * writes for the backward: states after every 8th scan position,
+ * (batch*ndir, ceil(seqlen/8), dim, 16).  Returns < 0 on a bad desc. */
 int64_t mvm_scan_ckpt_elems(const mvm_scan_desc* desc);
 
 /* Workspace bytes needed by mvm_scan_fwd (which = 0) or mvm_scan_bwd

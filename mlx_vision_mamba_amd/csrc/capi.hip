@@ -102,7 +102,7 @@ mvm::Geom make_geom(const mvm_scan_desc* d) {
   g.tok = d->seq_to_tok;
   g.chunk_len = pick_chunk_len(d);
   g.nchunk = d->seqlen > 0 ? ceil_div(d->seqlen, g.chunk_len) : 0;
-  g.nsub = ceil_div(d->seqlen, mvm::kSub);
+  g.nck = ceil_div(d->seqlen, mvm::kCk);
   g.ncblk = ceil_div(d->dim, mvm::kChPerBlock);
   return g;
 }
@@ -139,7 +139,7 @@ BwdWs bwd_ws(const mvm::Geom& g, bool recompute_ckpt) {
   w.part_dD = align_up(slots * sizeof(double));
   w.part_bc = align_up(static_cast<size_t>(g.B * g.K * g.ncblk * g.L) * 2 * mvm::kStatePad * sizeof(float));
   if (recompute_ckpt) {
-    w.ckpt = align_up(static_cast<size_t>(g.B * g.K * g.nsub * g.D) * mvm::kStatePad * sizeof(float));
+    w.ckpt = align_up(static_cast<size_t>(g.B * g.K * g.nck * g.D) * mvm::kStatePad * sizeof(float));
     w.fwd = fwd_ws(g).total;
   }
   w.total = w.agg_mu + w.agg_s + w.part_dA + w.part_dD + w.part_bc + w.ckpt + w.fwd;
@@ -168,7 +168,7 @@ int64_t mvm_scan_ckpt_elems(const mvm_scan_desc* desc) {
   const int rc = check_desc(desc);
   if (rc != MVM_OK) return rc;
   const mvm::Geom g = make_geom(desc);
-  return g.B * g.K * g.nsub * g.D * mvm::kStatePad;
+  return g.B * g.K * g.nck * g.D * mvm::kStatePad;
 }
 
 int64_t mvm_scan_workspace_bytes(const mvm_scan_desc* desc, int which) {

@@ -17,7 +17,9 @@
 // processed in reverse: the states h_{t-1}, h_t of the tile are recomputed
 // from the forward's checkpoint into VGPRs together with exp(delta A)
 // (one transcendental per element for the whole backward), then the adjoint
-// sweep runs over the registers.
+// sweep runs over the registers.  Inputs are staged tile by tile through
+// double-buffered LDS with coalesced loads issued one tile ahead; du, ddelta
+// and the dB | dC partials leave through LDS as coalesced rows.
 //
 // Reductions are atomic-free and in a fixed order (bitwise deterministic):
 //   dB, dC   sum over 16 channels per wave with cross-lane ops, over the 4
@@ -28,6 +30,8 @@
 //            partials per (b, chunk), summed in float64 by reduce_ad_kernel.
 // Long sequences: the adjoint carry between time chunks uses the same
 // two-pass idea as the forward, run right to left (bwd_agg + bwd_carry).
+#include <type_traits>
+
 #include "scan_common.h"
 #include "scan_kernels.h"
 
@@ -38,14 +42,18 @@ namespace mvm {
 template <typename XT>
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
-  __shared__ float sC[kSub][kStatePad];
+  __shared__ float sD[2][kSub][kChPerBlock];
+  __shared__ float sG[2][kSub][kChPerBlock];
+  __shared__ float sC[2][kSub][kStatePad];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int grp = lane & 3;
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * kChPerBlock + wave * kChPerWave + (lane >> 2);
+  const int cl = wave * kChPerWave + (lane >> 2);
+  const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
+  const int64_t d = ch0 + cl;
+  const int64_t dld = ch0 + (tid & 63);
   const bool dvalid = d < gm.D;
-  const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
@@ -53,7 +61,7 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xbase = b * gm.xsb + k * gm.xsk + dc;
+  const int64_t xrow = b * gm.xsb + k * gm.xsk;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
   const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
   const XT* __restrict__ dy = static_cast<const XT*>(bf.dy);
@@ -67,44 +75,48 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   }
   float dsum = 0.f;
   const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
-  for (int64_t it = ntile - 1; it >= 0; --it) {
-    const int64_t ts = t0 + it * kSub;
+  float pd[4], pg[4], pc;
+  {
+    const int64_t ts = t0 + (ntile - 1) * kSub;
+    const int nt = static_cast<int>(t1 - ts);
+    load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+    store_xtile(sD[0], pd, tid);
+    store_xtile(sG[0], pg, tid);
+    sC[0][tid >> 4][tid & 15] = pc;
+  }
+  for (int64_t j = 0; j < ntile; ++j) {
+    const int buf = static_cast<int>(j & 1);
+    const int64_t ts = t0 + (ntile - 1 - j) * kSub;
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
     __syncthreads();
-    for (int i = tid; i < kSub * kStatePad; i += kThreads) {
-      const int tt = i / kStatePad, n = i % kStatePad;
-      float v = 0.f;
-      if (tt < nt && n < gm.N) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        v = ld(Cm, bcbase + row * gm.bst + n);
-      }
-      sC[tt][n] = v;
-    }
-    __syncthreads();
-    float dl[kSub], gg[kSub];
-#pragma unroll
-    for (int tt = 0; tt < kSub; ++tt) {
-      dl[tt] = 0.f;
-      gg[tt] = 0.f;
-      if (tt < nt && dvalid) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        const int64_t off = xbase + row * gm.xst;
-        dl[tt] = bf.delta[off];
-        gg[tt] = ld(dy, off);
-      }
+    const bool more = j + 1 < ntile;
+    if (more) {
+      const int64_t tn = ts - kSub;
+      load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
     }
 #pragma unroll
     for (int tt = kSub - 1; tt >= 0; --tt) {
       if (tt < nt) {
-        const float4 c4 = *reinterpret_cast<const float4*>(&sC[tt][4 * grp]);
+        const float dl = sD[buf][tt][cl];
+        const float gy = sG[buf][tt][cl];
+        const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][tt][4 * grp]);
         const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lam = fmaf(cv[j], gg[tt], mu[j]);
-          mu[j] = fast_exp2(dl[tt] * a2[j]) * lam;
+        for (int jj = 0; jj < 4; ++jj) {
+          const float lam = fmaf(cv[jj], gy, mu[jj]);
+          mu[jj] = fast_exp2(dl * a2[jj]) * lam;
         }
-        dsum += dl[tt];
+        dsum += dl;
       }
+    }
+    if (more) {
+      store_xtile(sD[buf ^ 1], pd, tid);
+      store_xtile(sG[buf ^ 1], pg, tid);
+      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
     }
   }
   if (dvalid) {
@@ -140,18 +152,30 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
-// Pass 3: the reverse sweep.
+// Pass 3: the reverse sweep.  Each 16-step tile is processed as two 8-step
+// halves (later half first), each restarted from its checkpoint, so the
+// register tile is 9 x 4 states + 8 x 4 decays and three waves fit per SIMD.
 template <typename XT, typename OT>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 2)
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
-  __shared__ float sBC[2][kSub][kStatePad];
-  __shared__ float sRed[4][kSub][2][kStatePad];
+  // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
+  // written in place over u / delta of the same step once it is consumed;
+  // per-wave channel sums of dB | dC
+  __shared__ float sU[2][kSub][kChPerBlock];
+  __shared__ float sD[2][kSub][kChPerBlock];
+  __shared__ float sG[2][kSub][kChPerBlock];
+  __shared__ float sB[2][kSub][kStatePad];
+  __shared__ float sC[2][kSub][kStatePad];
+  __shared__ float sRed[2][4][kSub][2][kStatePad];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int grp = lane & 3;
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * kChPerBlock + wave * kChPerWave + (lane >> 2);
+  const int cl = wave * kChPerWave + (lane >> 2);
+  const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
+  const int64_t d = ch0 + cl;
+  const int64_t dld = ch0 + (tid & 63);
   const bool dvalid = d < gm.D;
   const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
@@ -161,7 +185,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xbase = b * gm.xsb + k * gm.xsk + dc;
+  const int64_t xrow = b * gm.xsb + k * gm.xsk;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -187,126 +211,174 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   }
   const float dskip = dvalid ? bf.Dv[k * gm.D + d] : 0.f;
   double dDacc = 0.0;
-  // lanes whose (channel-sum) result they publish: one per (g, j)
+  // state j = (lane >> 4) & 3 of the lane's group holds its channel sum
   const int red_j = (lane >> 4) & 3;
-  const bool red_writer = ((lane >> 2) & 3) == 0;
+  const float* ckb = bf.ckpt + (bk * gm.nck * gm.D + dc) * kStatePad + 4 * grp;
+  const int64_t ck_stride = gm.D * kStatePad;
 
-  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
-  for (int64_t it = ntile - 1; it >= 0; --it) {
-    const int64_t ts = t0 + it * kSub;
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
-    __syncthreads();  // previous tile's LDS readers are done
-    for (int i = tid; i < 2 * kSub * kStatePad; i += kThreads) {
-      const int which = i / (kSub * kStatePad);
-      const int tt = (i / kStatePad) % kSub;
-      const int n = i % kStatePad;
-      float v = 0.f;
-      if (tt < nt && n < gm.N) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        v = ld(which ? Cm : Bm, bcbase + row * gm.bst + n);
-      }
-      sBC[which][tt][n] = v;
-    }
-    __syncthreads();
-
-    float uu[kSub], dl[kSub], gg[kSub];
+  // state after position p - 1 (checkpoint slot p / 8 - 1), p a multiple of 8
+  auto load_ckpt = [&](int64_t p) {
+    float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p > 0 && dvalid) h4 = *reinterpret_cast<const float4*>(ckb + (p / kCk - 1) * ck_stride);
+    return h4;
+  };
+  // write back du / ddelta rows and this block's dB | dC partials of a tile
+  auto flush = [&](int buf, int64_t ts, int nt) {
+    const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lch = tid & 63;
 #pragma unroll
-    for (int tt = 0; tt < kSub; ++tt) {
-      uu[tt] = 0.f;
-      dl[tt] = 0.f;
-      gg[tt] = 0.f;
-      if (tt < nt && dvalid) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        const int64_t off = xbase + row * gm.xst;
-        uu[tt] = ld(u, off);
-        dl[tt] = bf.delta[off];
-        gg[tt] = ld(dy, off);
-      }
-    }
-
-    // states entering the tile: the checkpoint after position ts-1
-    float hs[kSub + 1][4];
-    if (ts > 0 && dvalid) {
-      const float4 h4 = *reinterpret_cast<const float4*>(
-          bf.ckpt + ((bk * gm.nsub + ts / kSub - 1) * gm.D + d) * kStatePad + 4 * grp);
-      hs[0][0] = h4.x; hs[0][1] = h4.y; hs[0][2] = h4.z; hs[0][3] = h4.w;
-    } else {
-      hs[0][0] = hs[0][1] = hs[0][2] = hs[0][3] = 0.f;
-    }
-    float ea[kSub][4];
-    // per-tile partial sums of dA / dD, added to the running totals once per
-    // tile (keeps fp32 rounding growth ~ tile + tiles, not chunk length)
-    float tacc[4] = {0.f, 0.f, 0.f, 0.f};
-    float tD = 0.f;
-#pragma unroll
-    for (int tt = 0; tt < kSub; ++tt) {
-      const float4 b4 = *reinterpret_cast<const float4*>(&sBC[0][tt][4 * grp]);
-      const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-      const float dxu = dl[tt] * uu[tt];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ea[tt][j] = fast_exp2(dl[tt] * a2[j]);
-        hs[tt + 1][j] = fmaf(ea[tt][j], hs[tt][j], dxu * bv[j]);
-      }
-    }
-
-#pragma unroll
-    for (int tt = kSub - 1; tt >= 0; --tt) {
+    for (int r = 0; r < 4; ++r) {
+      const int tt = wrow + 4 * r;
       if (tt < nt) {
-        const float4 b4 = *reinterpret_cast<const float4*>(&sBC[0][tt][4 * grp]);
-        const float4 c4 = *reinterpret_cast<const float4*>(&sBC[1][tt][4 * grp]);
-        const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
-        const float dxu = dl[tt] * uu[tt];
-        float sa = 0.f, sb = 0.f;
-        float xb[4], xc[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lam = fmaf(cv[j], gg[tt], mu[j]);
-          const float q = lam * ea[tt][j];
-          const float w = q * hs[tt][j];
-          sa = fmaf(w, an[j], sa);
-          tacc[j] = fmaf(w, dl[tt], tacc[j]);
-          sb = fmaf(lam, bv[j], sb);
-          xb[j] = lam * dxu;
-          xc[j] = gg[tt] * hs[tt + 1][j];
-          mu[j] = q;
-        }
-        sa = sum_groups(sa);
-        sb = sum_groups(sb);
-        tD = fmaf(gg[tt], uu[tt], tD);
-        if (grp == 0 && dvalid) {
-          const int64_t row = token_row(tok, ts + tt, gm.L);
-          const int64_t off = xbase + row * gm.xst;
-          st(du_out, off, fmaf(dl[tt], sb, dskip * gg[tt]));
-          bf.ddelta[off] = fmaf(uu[tt], sb, sa);
-        }
-        const float rb = channel_reduce4(xb[0], xb[1], xb[2], xb[3]);
-        const float rc = channel_reduce4(xc[0], xc[1], xc[2], xc[3]);
-        if (red_writer) {
-          sRed[wave][tt][0][4 * grp + red_j] = rb;
-          sRed[wave][tt][1][4 * grp + red_j] = rc;
+        const int64_t off = xrow + token_row(tok, ts + tt, gm.L) * gm.xst + ch0;
+        if (dld < gm.D) {
+          st(du_out + off, lch, sU[buf][tt][lch]);
+          bf.ddelta[off + lch] = sD[buf][tt][lch];
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dacc[j] += static_cast<double>(tacc[j]);
-    dDacc += static_cast<double>(tD);
-    __syncthreads();
-    // sum the 4 waves and publish this channel block's dB | dC partials
+    float* pbc = bf.part_bc + ((bk * gm.ncblk + blockIdx.x) * gm.L + ts) * (2 * kStatePad);
     for (int i = tid; i < nt * 2 * kStatePad; i += kThreads) {
       const int tt = i / (2 * kStatePad);
       const int w2 = (i / kStatePad) & 1;
       const int n = i % kStatePad;
-      const float s = (sRed[0][tt][w2][n] + sRed[1][tt][w2][n]) + (sRed[2][tt][w2][n] + sRed[3][tt][w2][n]);
-      bf.part_bc[((bk * gm.ncblk + blockIdx.x) * gm.L + ts + tt) * (2 * kStatePad) + w2 * kStatePad + n] = s;
+      pbc[i] = (sRed[buf][0][tt][w2][n] + sRed[buf][1][tt][w2][n]) +
+               (sRed[buf][2][tt][w2][n] + sRed[buf][3][tt][w2][n]);
+    }
+  };
+
+  float tacc[4], tD;
+  // reverse sweep over scan positions [h0, h0 + n) of tile buffer `buf`,
+  // entering with the state after position h0 - 1.  The step body has no
+  // divergent branches: lanes that share a result all store it.
+  auto half = [&](auto full, int buf, int h0, int n, float4 hin) {
+    constexpr bool kFull = decltype(full)::value;
+    float hs[kCk + 1][4];
+    float ea[kCk][4];
+    hs[0][0] = hin.x; hs[0][1] = hin.y; hs[0][2] = hin.z; hs[0][3] = hin.w;
+#pragma unroll
+    for (int i = 0; i < kCk; ++i) {
+      const int tt = h0 + i;
+      const float dl = sD[buf][tt][cl];
+      const float dxu = dl * sU[buf][tt][cl];
+      const float4 b4 = *reinterpret_cast<const float4*>(&sB[buf][tt][4 * grp]);
+      const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        ea[i][jj] = fast_exp2(dl * a2[jj]);
+        hs[i + 1][jj] = fmaf(ea[i][jj], hs[i][jj], dxu * bv[jj]);
+      }
+    }
+#pragma unroll
+    for (int i = kCk - 1; i >= 0; --i) {
+      if (kFull || i < n) {
+        const int tt = h0 + i;
+        const float uu = sU[buf][tt][cl];
+        const float dl = sD[buf][tt][cl];
+        const float gy = sG[buf][tt][cl];
+        const float4 b4 = *reinterpret_cast<const float4*>(&sB[buf][tt][4 * grp]);
+        const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][tt][4 * grp]);
+        const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+        const float dxu = dl * uu;
+        float sa = 0.f, sb = 0.f;
+        float xb[4], xc[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float lam = fmaf(cv[jj], gy, mu[jj]);
+          const float q = lam * ea[i][jj];
+          const float w = q * hs[i][jj];
+          sa = fmaf(w, an[jj], sa);
+          tacc[jj] = fmaf(w, dl, tacc[jj]);
+          sb = fmaf(lam, bv[jj], sb);
+          xb[jj] = lam * dxu;
+          xc[jj] = gy * hs[i + 1][jj];
+          mu[jj] = q;
+        }
+        sa = sum_groups(sa);
+        sb = sum_groups(sb);
+        tD = fmaf(gy, uu, tD);
+        // in place: this step's u / delta are consumed (the 4 lanes of the
+        // channel store the same values)
+        sU[buf][tt][cl] = fmaf(dl, sb, dskip * gy);
+        sD[buf][tt][cl] = fmaf(uu, sb, sa);
+        const float rb = channel_reduce4(xb[0], xb[1], xb[2], xb[3]);
+        const float rc = channel_reduce4(xc[0], xc[1], xc[2], xc[3]);
+        // lanes with equal (g, j) hold equal sums and store them together
+        sRed[buf][wave][tt][0][4 * grp + red_j] = rb;
+        sRed[buf][wave][tt][1][4 * grp + red_j] = rc;
+      }
+    }
+  };
+
+  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
+  float pu[4], pd[4], pg[4], pb, pc;
+  float4 pck0, pck1;  // checkpoints entering the two halves of the staged tile
+  {
+    const int64_t ts = t0 + (ntile - 1) * kSub;
+    const int nt = static_cast<int>(t1 - ts);
+    load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+    pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+    pck0 = load_ckpt(ts);
+    pck1 = load_ckpt(ts + kCk);
+    store_xtile(sU[0], pu, tid);
+    store_xtile(sD[0], pd, tid);
+    store_xtile(sG[0], pg, tid);
+    sB[0][tid >> 4][tid & 15] = pb;
+    sC[0][tid >> 4][tid & 15] = pc;
+  }
+
+  for (int64_t j = 0; j < ntile; ++j) {
+    const int buf = static_cast<int>(j & 1);
+    const int64_t ts = t0 + (ntile - 1 - j) * kSub;
+    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
+    __syncthreads();  // tile j staged; the previous tile's outputs are complete
+    if (j > 0) flush(buf ^ 1, ts + kSub, static_cast<int>(min<int64_t>(kSub, t1 - ts - kSub)));
+    const float4 hin0 = pck0, hin1 = pck1;
+    const bool more = j + 1 < ntile;
+    if (more) {  // prefetch the previous tile (next in processing order)
+      const int64_t tn = ts - kSub;
+      load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
+      pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
+      pck0 = load_ckpt(tn);
+      pck1 = load_ckpt(tn + kCk);
+    }
+    // per-tile partial sums of dA / dD, folded into float64 once per tile
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) tacc[jj] = 0.f;
+    tD = 0.f;
+    if (nt == kSub) {
+      half(std::true_type{}, buf, kCk, kCk, hin1);
+      half(std::true_type{}, buf, 0, kCk, hin0);
+    } else {
+      if (nt > kCk) half(std::false_type{}, buf, kCk, nt - kCk, hin1);
+      half(std::false_type{}, buf, 0, nt < kCk ? nt : kCk, hin0);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dacc[jj] += static_cast<double>(tacc[jj]);
+    dDacc += static_cast<double>(tD);
+    if (more) {
+      __syncthreads();  // all flushes of the other buffer are done before it is refilled
+      store_xtile(sU[buf ^ 1], pu, tid);
+      store_xtile(sD[buf ^ 1], pd, tid);
+      store_xtile(sG[buf ^ 1], pg, tid);
+      sB[buf ^ 1][tid >> 4][tid & 15] = pb;
+      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
     }
   }
+  __syncthreads();
+  flush(static_cast<int>((ntile - 1) & 1), t0, static_cast<int>(min<int64_t>(kSub, t1 - t0)));
 
   if (dvalid) {
     double* pa = bf.part_dA + slot * kStatePad + 4 * grp;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pa[j] = dacc[j];
+    for (int jj = 0; jj < 4; ++jj) pa[jj] = dacc[jj];
     if (grp == 0) bf.part_dD[slot] = dDacc;
   }
 }

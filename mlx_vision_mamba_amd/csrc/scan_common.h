@@ -14,7 +14,8 @@
 
 namespace mvm {
 
-constexpr int kSub = 16;          // scan positions per tile == checkpoint interval
+constexpr int kSub = 16;          // scan positions per staged tile
+constexpr int kCk = 8;            // checkpoint interval (half a tile)
 constexpr int kThreads = 256;     // threads per workgroup (4 waves)
 constexpr int kChPerWave = 16;
 constexpr int kChPerBlock = 64;
@@ -85,28 +86,34 @@ __device__ __forceinline__ float sum_groups(float x) {
   return x;
 }
 
-// v_permlane32_swap / v_permlane16_swap are issued through inline asm with
-// both registers as in/out operands: this toolchain's
-// __builtin_amdgcn_permlane{16,32}_swap keeps only element 0 of the
-// intrinsic's {vdst, vsrc} result and returns it for both halves.  The
-// leading s_nop 1 gives the two wait states a permlane needs after a VALU
-// write of its operands (the compiler inserts the same for the builtin).
+// v_permlane{32,16}_swap return both swapped registers.  The builtin's two
+// results are read through a 64-bit bit_cast: in this toolchain, indexing
+// the returned vector (r[1]) re-reads element 0, so the second half would be
+// lost.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a),
+                                                 __builtin_bit_cast(unsigned, b), false, false);
+  const unsigned long long w = __builtin_bit_cast(unsigned long long, r);
+  return __builtin_bit_cast(float, static_cast<unsigned>(w)) +
+         __builtin_bit_cast(float, static_cast<unsigned>(w >> 32));
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a),
+                                                 __builtin_bit_cast(unsigned, b), false, false);
+  const unsigned long long w = __builtin_bit_cast(unsigned long long, r);
+  return __builtin_bit_cast(float, static_cast<unsigned>(w)) +
+         __builtin_bit_cast(float, static_cast<unsigned>(w >> 32));
+}
 
 // v_permlane32_swap: lanes 32..63 of `a` trade places with lanes 0..31 of
 // `b`.  Afterwards a + b holds, in lanes 0..31, a summed over lanes (l, l+32)
 // and, in lanes 32..63, b summed over (l-32, l).
-__device__ __forceinline__ float pair_reduce32(float a, float b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
-}
+__device__ __forceinline__ float pair_reduce32(float a, float b) { return swap_sum32(a, b); }
 
 // v_permlane16_swap: odd 16-lane rows of `a` trade places with even rows of
 // `b`.  Afterwards a + b holds, in rows 0 and 2, a summed over row pairs
 // (0,1) / (2,3) and, in rows 1 and 3, b summed over the same pairs.
-__device__ __forceinline__ float pair_reduce16(float a, float b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return a + b;
-}
+__device__ __forceinline__ float pair_reduce16(float a, float b) { return swap_sum16(a, b); }
 
 // Sum over the 16 channels of a wave of four per-lane values v[0..3] (the
 // lane's states 4g+j).  Returns, in lane (c, g) with j = (lane >> 4) & 3, the
@@ -118,6 +125,47 @@ __device__ __forceinline__ float channel_reduce4(float v0, float v1, float v2, f
   s += dpp<kRowRor8>(s);                    // lane bit 3
   s += dpp<kRowRor4>(s);                    // lane bit 2
   return s;
+}
+
+// ------------------------------------------------------ tile staging
+// A tile is kSub consecutive scan positions of one workgroup's 64 channels.
+// Channel-indexed tensors are loaded fully coalesced: thread i holds scan
+// positions (i >> 6) + 4r, r = 0..3, of channel (i & 63), so every wave
+// reads 64 consecutive channels of one token row per instruction.
+// State-indexed tensors (B, C): thread i holds position i >> 4, state i & 15.
+
+template <typename T>
+__device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ p, int64_t base,
+                                           int64_t ch, int64_t D, int64_t xst,
+                                           const int32_t* tok, int64_t ts, int nt, int64_t L,
+                                           int tid) {
+  // the row of each load is wave-uniform: keep its pointer in SGPRs and use
+  // a 32-bit per-lane channel offset
+  const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lch = tid & 63;
+  const bool cok = ch < D;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int tt = wrow + 4 * r;
+    v[r] = 0.f;
+    if (tt < nt) {
+      const T* rowp = p + (base + token_row(tok, ts + tt, L) * xst + (ch - lch));
+      if (cok) v[r] = to_f32(rowp[lch]);
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base, int64_t N,
+                                            int64_t bst, const int32_t* tok, int64_t ts, int nt,
+                                            int64_t L, int tid) {
+  const int tt = tid >> 4, n = tid & 15;
+  return (tt < nt && n < N) ? ld(p, base + token_row(tok, ts + tt, L) * bst + n) : 0.f;
+}
+
+__device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float (&v)[4], int tid) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) s[(tid >> 6) + 4 * r][tid & 63] = v[r];
 }
 
 }  // namespace mvm

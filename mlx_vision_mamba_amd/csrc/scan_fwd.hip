@@ -6,9 +6,12 @@
 //
 // Work split.  Lane (c, g) of a wave owns states 4g..4g+3 of one channel
 // (scan_common.h).  A 256-thread workgroup covers 64 channels of one
-// (batch, direction) pair and one time chunk.  Per 16-step tile the
-// workgroup stages B_t / C_t (shared by all its channels) in LDS, converted
-// to fp32 once; u and delta are read straight from HBM, channel-contiguous.
+// (batch, direction) pair and one time chunk, walking it in 16-step tiles.
+// Each tile of u, delta (64 channels) and B, C (16 states, shared by all
+// channels) is loaded with fully coalesced reads into a double-buffered LDS
+// stage, converted to fp32 once; the next tile's loads are issued before the
+// current tile's math so their latency is hidden.  y goes through LDS too
+// and is written back one tile later as coalesced rows.
 //
 // Long sequences are split into time chunks so that the grid fills the
 // chip (the two-pass scheme whose carry step the reference left as TODO at
@@ -18,7 +21,7 @@
 //   pass 2 (carry)   one thread per (b, k, d, n) folds the aggregates in
 //                    order: H_c = exp(A*S_c) * H_{c-1} + e_c (mamba_fast.py:85-86);
 //   pass 3 (kMain)   each chunk rescans from its carry-in, writes y and,
-//                    when training, the state after every 16th position
+//                    when training, the state after every 8th position
 //                    (the backward's checkpoints).
 #include "scan_common.h"
 #include "scan_kernels.h"
@@ -30,13 +33,22 @@ enum FwdMode { kAgg = 0, kMain = 1 };
 template <typename XT, typename OT, int MODE>
 __global__ void __launch_bounds__(kThreads)
 scan_fwd_kernel(Geom gm, FwdBufs bf) {
-  __shared__ float sBC[2][kSub][kStatePad];
+  // double-buffered tile staging: u, delta (64 channels), B, C (16 states),
+  // and y (written back coalesced one tile later)
+  __shared__ float sU[2][kSub][kChPerBlock];
+  __shared__ float sD[2][kSub][kChPerBlock];
+  __shared__ float sB[2][kSub][kStatePad];
+  __shared__ float sC[2][kSub][kStatePad];
+  __shared__ float sY[2][kSub][kChPerBlock];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int grp = lane & 3;
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * kChPerBlock + wave * kChPerWave + (lane >> 2);
+  const int cl = wave * kChPerWave + (lane >> 2);          // compute channel within the block
+  const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
+  const int64_t d = ch0 + cl;
+  const int64_t dld = ch0 + (tid & 63);                    // channel this thread loads / stores
   const bool dvalid = d < gm.D;
   const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
@@ -46,7 +58,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xbase = b * gm.xsb + k * gm.xsk + dc;
+  const int64_t xrow = b * gm.xsb + k * gm.xsk;            // + row * xst + channel
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -54,6 +66,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm);
   const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
   OT* __restrict__ y = static_cast<OT*>(bf.y);
+  float* __restrict__ ckpt = bf.ckpt;
 
   float a2[4], h[4];
 #pragma unroll
@@ -69,70 +82,104 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     h[0] = c4.x; h[1] = c4.y; h[2] = c4.z; h[3] = c4.w;
   }
   float dsum = 0.f;
-
-  for (int64_t ts = t0; ts < t1; ts += kSub) {
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
-    __syncthreads();  // the previous tile's LDS readers are done
-    constexpr int kStage = (MODE == kMain ? 2 : 1) * kSub * kStatePad;
-    for (int i = tid; i < kStage; i += kThreads) {
-      const int which = i / (kSub * kStatePad);
-      const int tt = (i / kStatePad) % kSub;
-      const int n = i % kStatePad;
-      float v = 0.f;
-      if (tt < nt && n < gm.N) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        v = ld(which ? Cm : Bm, bcbase + row * gm.bst + n);
-      }
-      sBC[which][tt][n] = v;
-    }
-    __syncthreads();
-
-    float uu[kSub], dl[kSub];
+  const bool write_y = MODE == kMain && y != nullptr;
+  const bool write_ck = MODE == kMain && ckpt != nullptr && dvalid;
+  // checkpoint slot s holds the state after position 8s + 7
+  float* ckp = write_ck ? ckpt + (bk * gm.nck * gm.D + d) * kStatePad + 4 * grp : nullptr;
+  const int64_t ck_stride = gm.D * kStatePad;
+  auto flush_y = [&](int buf, int64_t ts, int nt) {
+    const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lch = tid & 63;
 #pragma unroll
-    for (int tt = 0; tt < kSub; ++tt) {
-      uu[tt] = 0.f;
-      dl[tt] = 0.f;
-      if (tt < nt && dvalid) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        const int64_t off = xbase + row * gm.xst;
-        uu[tt] = ld(u, off);
-        dl[tt] = delta[off];
-      }
-    }
-
-#pragma unroll
-    for (int tt = 0; tt < kSub; ++tt) {
+    for (int r = 0; r < 4; ++r) {
+      const int tt = wrow + 4 * r;
       if (tt < nt) {
-        const float4 b4 = *reinterpret_cast<const float4*>(&sBC[0][tt][4 * grp]);
-        const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-        const float du = dl[tt] * uu[tt];
-        float yp = 0.f;
-        float cv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (MODE == kMain) {
-          const float4 c4 = *reinterpret_cast<const float4*>(&sBC[1][tt][4 * grp]);
-          cv[0] = c4.x; cv[1] = c4.y; cv[2] = c4.z; cv[3] = c4.w;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e = fast_exp2(dl[tt] * a2[j]);
-          h[j] = fmaf(e, h[j], du * bv[j]);
-          if (MODE == kMain) yp = fmaf(cv[j], h[j], yp);
-        }
-        if (MODE == kAgg) dsum += dl[tt];
-        if (MODE == kMain) {
-          yp = sum_groups(yp);
-          if (y != nullptr && grp == 0 && dvalid) {
-            const int64_t row = token_row(tok, ts + tt, gm.L);
-            st(y, xbase + row * gm.xst, fmaf(dskip, uu[tt], yp));
-          }
-        }
+        OT* rowp = y + (xrow + token_row(tok, ts + tt, gm.L) * gm.xst + ch0);
+        if (dld < gm.D) st(rowp, lch, sY[buf][tt][lch]);
       }
     }
-    if (MODE == kMain && bf.ckpt != nullptr && dvalid) {
-      float4 c4 = make_float4(h[0], h[1], h[2], h[3]);
-      *reinterpret_cast<float4*>(bf.ckpt + ((bk * gm.nsub + ts / kSub) * gm.D + d) * kStatePad +
-                                 4 * grp) = c4;
+  };
+  // one scan step at tile position tt of buffer buf
+  auto step = [&](int buf, int tt) {
+    const float uu = sU[buf][tt][cl];
+    const float dl = sD[buf][tt][cl];
+    const float4 b4 = *reinterpret_cast<const float4*>(&sB[buf][tt][4 * grp]);
+    const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+    const float du = dl * uu;
+    float yp = 0.f;
+    float cv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (MODE == kMain) {
+      const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][tt][4 * grp]);
+      cv[0] = c4.x; cv[1] = c4.y; cv[2] = c4.z; cv[3] = c4.w;
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e = fast_exp2(dl * a2[j]);
+      h[j] = fmaf(e, h[j], du * bv[j]);
+      if (MODE == kMain) yp = fmaf(cv[j], h[j], yp);
+    }
+    if (MODE == kAgg) dsum += dl;
+    if (MODE == kMain) {  // the channel's 4 lanes store the same y (no branch)
+      yp = sum_groups(yp);
+      sY[buf][tt][cl] = fmaf(dskip, uu, yp);
+    }
+  };
+  auto store_ck = [&](int64_t pos_end) {  // state after position pos_end (== 8s + 7)
+    *reinterpret_cast<float4*>(ckp + (pos_end / kCk) * ck_stride) = make_float4(h[0], h[1], h[2], h[3]);
+  };
+
+  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
+  float pu[4], pd[4], pb = 0.f, pc = 0.f;
+  {
+    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - t0));
+    load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, t0, nt, gm.L, tid);
+    load_xtile(pd, delta, xrow, dld, gm.D, gm.xst, tok, t0, nt, gm.L, tid);
+    pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
+    if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
+    store_xtile(sU[0], pu, tid);
+    store_xtile(sD[0], pd, tid);
+    sB[0][tid >> 4][tid & 15] = pb;
+    sC[0][tid >> 4][tid & 15] = pc;
+  }
+
+  for (int64_t it = 0; it < ntile; ++it) {
+    const int buf = static_cast<int>(it & 1);
+    const int64_t ts = t0 + it * kSub;
+    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
+    __syncthreads();  // tile `it` staged; readers of the other buffer are done
+    if (write_y && it > 0) flush_y(buf ^ 1, ts - kSub, kSub);
+    const bool more = it + 1 < ntile;
+    if (more) {  // prefetch the next tile; its latency overlaps this tile's math
+      const int64_t tn = ts + kSub;
+      const int ntn = static_cast<int>(min<int64_t>(kSub, t1 - tn));
+      load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, ntn, gm.L, tid);
+      load_xtile(pd, delta, xrow, dld, gm.D, gm.xst, tok, tn, ntn, gm.L, tid);
+      pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
+      if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
+    }
+    if (nt == kSub) {  // full tile: no per-step bounds checks
+#pragma unroll
+      for (int tt = 0; tt < kSub; ++tt) {
+        step(buf, tt);
+        if (write_ck && (tt == kCk - 1 || tt == kSub - 1)) store_ck(ts + tt);
+      }
+    } else {
+      for (int tt = 0; tt < nt; ++tt) {
+        step(buf, tt);
+        if (write_ck && tt == kCk - 1) store_ck(ts + tt);
+      }
+    }
+    if (more) {
+      store_xtile(sU[buf ^ 1], pu, tid);
+      store_xtile(sD[buf ^ 1], pd, tid);
+      sB[buf ^ 1][tid >> 4][tid & 15] = pb;
+      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
+    }
+  }
+  if (write_y) {
+    __syncthreads();
+    const int64_t ts = t0 + (ntile - 1) * kSub;
+    flush_y(static_cast<int>((ntile - 1) & 1), ts, static_cast<int>(t1 - ts));
   }
 
   if (MODE == kAgg && dvalid) {

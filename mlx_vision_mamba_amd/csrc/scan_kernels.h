@@ -15,7 +15,7 @@ struct Geom {
   const int32_t* tok;      // (K, L) scan position -> token row, or nullptr
   int64_t chunk_len;       // multiple of kSub
   int64_t nchunk;          // ceil(L / chunk_len)
-  int64_t nsub;            // ceil(L / kSub), checkpoint slots per (b, k, d)
+  int64_t nck;             // ceil(L / kCk), checkpoint slots per (b, k, d)
   int64_t ncblk;           // ceil(D / 64), channel blocks
 };
 

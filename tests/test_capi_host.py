@@ -71,7 +71,7 @@ def test_valid_desc_and_sizes():
     d = _desc()
     assert _validate(d) == 0
     lib = _lib.lib()
-    assert lib.mvm_scan_ckpt_elems(ctypes.byref(d)) == 2 * 1 * 3 * 24 * 16   # ceil(40/16)=3
+    assert lib.mvm_scan_ckpt_elems(ctypes.byref(d)) == 2 * 1 * 5 * 24 * 16   # ceil(40/8)=5
     assert lib.mvm_scan_chunk_len(ctypes.byref(d)) % 16 == 0
     for which in (0, 1, 2):
         assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), which) >= 0
