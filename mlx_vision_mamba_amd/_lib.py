@@ -43,8 +43,19 @@ class ScanDesc(ctypes.Structure):
     ]
 
 
-# symbol -> (restype, argtypes); every entry point of include/mvm_scan.h and
-# the test hook of include/mvm_testing.h
+class ConvDesc(ctypes.Structure):
+    """Mirror of ``mvm_conv_desc`` (include/mvm_conv.h)."""
+
+    _fields_ = [
+        ("batch", _i64), ("seqlen", _i64), ("dim", _i64), ("ndir", _i64), ("kwidth", _i64),
+        ("x_stride_b", _i64), ("x_stride_k", _i64), ("x_stride_t", _i64),
+        ("y_stride_b", _i64), ("y_stride_k", _i64), ("y_stride_t", _i64),
+        ("seq_to_tok", _vp),
+    ]
+
+
+# symbol -> (restype, argtypes); every entry point of include/mvm_scan.h,
+# include/mvm_conv.h and the test hook of include/mvm_testing.h
 SIGNATURES = {
     "mvm_abi_version": (ctypes.c_int, []),
     "mvm_last_error": (ctypes.c_char_p, []),
@@ -54,6 +65,10 @@ SIGNATURES = {
     "mvm_scan_chunk_len": (_i64, [ctypes.POINTER(ScanDesc)]),
     "mvm_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 9 + [ctypes.c_size_t, _vp]),
     "mvm_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 15 + [ctypes.c_size_t, _vp]),
+    "mvm_conv_validate": (ctypes.c_int, [ctypes.POINTER(ConvDesc)]),
+    "mvm_conv_workspace_bytes": (_i64, [ctypes.POINTER(ConvDesc)]),
+    "mvm_conv_silu_fwd": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [_vp] * 5),
+    "mvm_conv_silu_bwd": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [_vp] * 8 + [ctypes.c_size_t, _vp]),
     "mvm_selftest_lanes": (ctypes.c_int, [_vp, _vp]),
 }
 

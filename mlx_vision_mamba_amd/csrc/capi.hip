@@ -10,6 +10,8 @@
 
 #include <algorithm>
 
+#include "conv_kernels.h"
+#include "mvm_conv.h"
 #include "mvm_scan.h"
 #include "mvm_testing.h"
 #include "scan_common.h"
@@ -279,6 +281,88 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta, c
   mvm::BwdBufs b{u, delta, A, Bm, Cm, Dv, ckpt, dy, du, ddelta, dA, dB, dC, dD,
                  agg_mu, agg_s, part_dA, part_dD, part_bc};
   return hip_status(mvm::launch_bwd(g, b, desc->in_dtype, desc->out_dtype, s), "mvm_scan_bwd launch");
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_conv(const mvm_conv_desc* d) {
+  if (d == nullptr) return fail(MVM_ERR_INVALID_ARG, "conv desc is NULL");
+  if (d->batch < 0 || d->seqlen < 0 || d->dim < 0)
+    return fail(MVM_ERR_INVALID_ARG, "negative size in conv desc");
+  if (d->ndir < 1) return fail(MVM_ERR_INVALID_ARG, "conv ndir=%lld must be >= 1", (long long)d->ndir);
+  if (d->kwidth < 1 || d->kwidth > MVM_CONV_MAX_KWIDTH)
+    return fail(MVM_ERR_UNSUPPORTED, "kwidth=%lld unsupported (1..%d)", (long long)d->kwidth,
+                MVM_CONV_MAX_KWIDTH);
+  const int64_t st[6] = {d->x_stride_b, d->x_stride_k, d->x_stride_t,
+                         d->y_stride_b, d->y_stride_k, d->y_stride_t};
+  for (int64_t v : st)
+    if (v < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride in conv desc");
+  if (d->seqlen > 1 && (d->x_stride_t < d->dim || d->y_stride_t < d->dim))
+    return fail(MVM_ERR_INVALID_ARG, "conv row stride overlaps channels");
+  if (d->batch * d->ndir > 65535) return fail(MVM_ERR_UNSUPPORTED, "batch*ndir exceeds 65535");
+  return MVM_OK;
+}
+
+mvm::ConvGeom conv_geom(const mvm_conv_desc* d) {
+  mvm::ConvGeom g;
+  g.B = d->batch; g.L = d->seqlen; g.D = d->dim; g.K = d->ndir;
+  g.xsb = d->x_stride_b; g.xsk = d->x_stride_k; g.xst = d->x_stride_t;
+  g.ysb = d->y_stride_b; g.ysk = d->y_stride_k; g.yst = d->y_stride_t;
+  g.tok = d->seq_to_tok;
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvm_conv_validate(const mvm_conv_desc* desc) {
+  const int rc = check_conv(desc);
+  return rc == MVM_OK ? ok() : rc;
+}
+
+int64_t mvm_conv_workspace_bytes(const mvm_conv_desc* desc) {
+  const int rc = check_conv(desc);
+  if (rc != MVM_OK) return rc;
+  return static_cast<int64_t>(
+      align_up(sizeof(float) * mvm::conv_partial_floats(conv_geom(desc), static_cast<int>(desc->kwidth))));
+}
+
+int mvm_conv_silu_fwd(const mvm_conv_desc* desc, const float* x, const float* w,
+                      const float* bias, float* y, void* stream) {
+  const int rc = check_conv(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::ConvGeom g = conv_geom(desc);
+  if (g.B == 0 || g.L == 0 || g.D == 0) return ok();
+  if (!x || !w || !bias || !y) return fail(MVM_ERR_INVALID_ARG, "mvm_conv_silu_fwd: NULL pointer");
+  return hip_status(mvm::launch_conv_fwd(g, static_cast<int>(desc->kwidth), x, w, bias, y,
+                                         static_cast<hipStream_t>(stream)),
+                    "mvm_conv_silu_fwd launch");
+}
+
+int mvm_conv_silu_bwd(const mvm_conv_desc* desc, const float* x, const float* w,
+                      const float* bias, const float* dy, float* dx, float* dw, float* dbias,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = check_conv(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::ConvGeom g = conv_geom(desc);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int kc = static_cast<int>(desc->kwidth);
+  if (g.D > 0 && (!dw || !dbias)) return fail(MVM_ERR_INVALID_ARG, "mvm_conv_silu_bwd: NULL dw/dbias");
+  if (g.B == 0 || g.L == 0 || g.D == 0) {
+    hipError_t e = mvm::launch_fill(dw, g.K * g.D * kc, 0.f, s);
+    if (e == hipSuccess) e = mvm::launch_fill(dbias, g.K * g.D, 0.f, s);
+    return hip_status(e, "mvm_conv_silu_bwd fill");
+  }
+  if (!x || !w || !bias || !dy || !dx) return fail(MVM_ERR_INVALID_ARG, "mvm_conv_silu_bwd: NULL pointer");
+  const size_t need = align_up(sizeof(float) * mvm::conv_partial_floats(g, kc));
+  if (workspace_bytes < need || workspace == nullptr)
+    return fail(MVM_ERR_WORKSPACE, "mvm_conv_silu_bwd: workspace %zu bytes < %zu needed", workspace_bytes, need);
+  return hip_status(mvm::launch_conv_bwd(g, kc, x, w, bias, dy, dx, dw, dbias,
+                                         static_cast<float*>(workspace), s),
+                    "mvm_conv_silu_bwd launch");
 }
 
 int mvm_selftest_lanes(float* out, void* stream) {

@@ -26,6 +26,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import directions as _dirs
+from .conv import causal_conv_silu
 from .scan import get_scan_fn, mode_chunk_len, selective_scan_directions
 
 
@@ -151,28 +152,6 @@ def _cached_table(cache, K, n, grid, device):
     return cache[key]
 
 
-def _causal_conv(xb, tok, weight, bias, d_conv):
-    """Causal depthwise conv along each direction's scan order.
-
-    xb: (B, N, K, Din) token order; tok: (K, N) or None; weight (K*Din, 1,
-    d_conv); bias (K*Din).  Output position s of direction k sees inputs at
-    scan positions s-d_conv+1 .. s (MLX Conv1d with symmetric padding then
-    [:, :L], mamba_block.py:129-132, :170).
-    """
-    bsz, n, K, din = xb.shape
-    if tok is not None:
-        seq = torch.stack([xb[:, tok[k].long(), k, :] for k in range(K)], dim=2)
-    else:
-        seq = xb
-    y = F.conv1d(seq.permute(0, 2, 3, 1).reshape(bsz, K * din, n), weight, bias,
-                 padding=d_conv - 1, groups=K * din)[..., :n]
-    y = y.reshape(bsz, K, din, n).permute(0, 3, 1, 2)
-    if tok is not None:
-        inv = _dirs.inverse_table(tok)
-        y = torch.stack([y[:, inv[k].long(), k, :] for k in range(K)], dim=2)
-    return y
-
-
 def _directional_forward(blocks, h, tok, scan_mode):
     """Run len(blocks) MambaBlocks on one (B, N, E) input, block k scanning
     in the order of tok[k], and return the sum of their outputs."""
@@ -183,9 +162,9 @@ def _directional_forward(blocks, h, tok, scan_mode):
     W_in = torch.cat([blk.in_proj.weight for blk in blocks], 0) if K > 1 else b0.in_proj.weight
     xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165
     xb, z = xz[..., :din], xz[..., din:]                                       # :166-167
-    conv_w = torch.cat([blk.conv1d.weight for blk in blocks], 0)
-    conv_b = torch.cat([blk.conv1d.bias for blk in blocks], 0)
-    xc = F.silu(_causal_conv(xb, tok, conv_w, conv_b, b0.d_conv))              # :170-171
+    conv_w = torch.cat([blk.conv1d.weight for blk in blocks], 0).view(K, din, b0.d_conv)
+    conv_b = torch.cat([blk.conv1d.bias for blk in blocks], 0).view(K, din)
+    xc = causal_conv_silu(xb, conv_w, conv_b, tok)                             # :170-171
     W_x = torch.stack([blk.x_proj.weight for blk in blocks], 0)                # (K, R+2N, Din)
     dbc = torch.matmul(xc.permute(2, 0, 1, 3).reshape(K, bsz * n, din),
                        W_x.transpose(1, 2).contiguous())                       # :174

@@ -19,7 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared_functions():
     names = []
-    for hdr in ("mvm_scan.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(", text)
@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 def _header_arity():
     """Parameter count of every function declared in the headers."""
     out = {}
-    for hdr in ("mvm_scan.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for name, params in re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
@@ -153,3 +153,36 @@ def test_shape_errors():
     with pytest.raises(ValueError):
         scan.scan_forward(torch.zeros(1, 2, 1, 3), torch.zeros(1, 2, 1, 3), torch.zeros(1, 3, 17),
                           torch.zeros(1, 2, 1, 17), torch.zeros(1, 2, 1, 17), torch.zeros(1, 3))
+
+
+def _cdesc(B=2, L=20, D=24, K=1, kc=4):
+    d = _lib.ConvDesc()
+    d.batch, d.seqlen, d.dim, d.ndir, d.kwidth = B, L, D, K, kc
+    d.x_stride_b, d.x_stride_t, d.x_stride_k = L * K * 2 * D, K * 2 * D, 2 * D
+    d.y_stride_b, d.y_stride_t, d.y_stride_k = L * K * D, K * D, D
+    return d
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("kwidth", 9, _lib.MVM_ERR_UNSUPPORTED), ("kwidth", 0, _lib.MVM_ERR_UNSUPPORTED),
+    ("ndir", 0, _lib.MVM_ERR_INVALID_ARG), ("batch", -2, _lib.MVM_ERR_INVALID_ARG),
+    ("y_stride_t", 3, _lib.MVM_ERR_INVALID_ARG), ("x_stride_k", -1, _lib.MVM_ERR_INVALID_ARG),
+])
+def test_conv_bad_descriptors_rejected(field, value, code):
+    lib = _lib.lib()
+    d = _cdesc()
+    assert lib.mvm_conv_validate(ctypes.byref(d)) == 0
+    assert lib.mvm_conv_workspace_bytes(ctypes.byref(d)) > 0
+    setattr(d, field, value)
+    assert lib.mvm_conv_validate(ctypes.byref(d)) == code
+
+
+def test_conv_null_and_workspace_rejected_before_launch():
+    lib = _lib.lib()
+    d = _cdesc()
+    null = ctypes.c_void_p(0)
+    assert lib.mvm_conv_silu_fwd(ctypes.byref(d), *([null] * 5)) == _lib.MVM_ERR_INVALID_ARG
+    fake = ctypes.c_void_p(0x1000)
+    need = lib.mvm_conv_workspace_bytes(ctypes.byref(d))
+    rc = lib.mvm_conv_silu_bwd(ctypes.byref(d), *([fake] * 8), need - 1, null)
+    assert rc == _lib.MVM_ERR_WORKSPACE

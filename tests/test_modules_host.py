@@ -26,32 +26,6 @@ def test_tables_match_oracle(K, grid):
         np.testing.assert_array_equal(table[k][inv[k].long()].numpy(), np.arange(n))
 
 
-@pytest.mark.parametrize("K,grid", [(2, None), (4, (3, 4)), (6, (2, 3, 2)), (8, (2, 1, 3, 2))])
-def test_remapped_causal_conv_matches_materialised_permutation(K, grid):
-    torch.manual_seed(0)
-    n = int(np.prod(grid)) if grid else 9
-    bsz, din, kc = 2, 5, 4
-    xb = torch.randn(bsz, n, K, din, dtype=torch.float64)
-    w = torch.randn(K * din, 1, kc, dtype=torch.float64)
-    b = torch.randn(K * din, dtype=torch.float64)
-    tok = dirs.seq_to_tok_table(K, n, grid)
-    got = mb._causal_conv(xb, tok, w, b, kc)
-    for k in range(K):
-        axes, rev = so.direction_axis_order(K, k)
-        seq = xb[:, :, k, :]
-        if axes is not None:
-            seq = torch_ref._permute(seq, grid, axes)
-        if rev:
-            seq = seq.flip(1)
-        out = F.conv1d(seq.transpose(1, 2), w[k * din:(k + 1) * din], b[k * din:(k + 1) * din],
-                       padding=kc - 1, groups=din)[..., :n].transpose(1, 2)
-        if rev:
-            out = out.flip(1)
-        if axes is not None:
-            out = torch_ref._unpermute(out, grid, axes)
-        torch.testing.assert_close(got[:, :, k, :], out, rtol=1e-12, atol=1e-12)
-
-
 def test_patch_embeds_equal_strided_convolution():
     torch.manual_seed(1)
     pe = vit.PatchEmbed(3, 8, 4).double()
