@@ -54,12 +54,15 @@ __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i])
 template <typename T>
 __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 
-// Token row read / written at scan position t.  Table entries are clamped
-// to [0, L) so that a malformed remap table cannot address outside the
-// tensors (the clamp is scalar work on a wave-uniform value).
+// Token row read / written at scan position t.  The table is read through
+// the constant address space, so a wave-uniform lookup is a scalar load
+// (K$, lgkmcnt) and never waits behind the vector loads in flight.  Table
+// entries are clamped to [0, L) so that a malformed remap table cannot
+// address outside the tensors (scalar work on a wave-uniform value).
+typedef __attribute__((address_space(4))) const int32_t const_i32;
 __device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int64_t L) {
   if (tok == nullptr) return t;
-  const int64_t r = tok[t];
+  const int64_t r = ((const const_i32*)tok)[t];  // generic -> constant addrspacecast
   return r < 0 ? 0 : (r >= L ? L - 1 : r);
 }
 
@@ -159,8 +162,16 @@ template <typename T>
 __device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base, int64_t N,
                                             int64_t bst, const int32_t* tok, int64_t ts, int nt,
                                             int64_t L, int tid) {
+  // a wave covers 4 consecutive positions (16 lanes each): look their rows
+  // up with wave-uniform (scalar) loads, then pick this lane's quarter
   const int tt = tid >> 4, n = tid & 15;
-  return (tt < nt && n < N) ? ld(p, base + token_row(tok, ts + tt, L) * bst + n) : 0.f;
+  const int w4 = __builtin_amdgcn_readfirstlane(tid >> 6) * 4;
+  int64_t rows[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) rows[q] = (w4 + q < nt) ? token_row(tok, ts + w4 + q, L) : 0;
+  const int q = tt & 3;
+  const int64_t row = q == 0 ? rows[0] : (q == 1 ? rows[1] : (q == 2 ? rows[2] : rows[3]));
+  return (tt < nt && n < N) ? ld(p, base + row * bst + n) : 0.f;
 }
 
 __device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float (&v)[4], int tid) {
