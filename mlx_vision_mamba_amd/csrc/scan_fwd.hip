@@ -10,8 +10,11 @@
 // Each tile of u, delta (64 channels) and B, C (16 states, shared by all
 // channels) is loaded with fully coalesced reads into a double-buffered LDS
 // stage, converted to fp32 once; the next tile's loads are issued before the
-// current tile's math so their latency is hidden.  y goes through LDS too
-// and is written back one tile later as coalesced rows.
+// current tile's math so their latency is hidden.  y replaces u in the LDS
+// stage and is written back one tile later as coalesced rows.  20 KiB of
+// LDS and <= 80 VGPRs per block let six 4-wave blocks share a CU, so a
+// VisionMamba-sized grid (B*K*D/64 = 1536 blocks) runs in one wave of
+// blocks on 256 CUs.
 //
 // Long sequences are split into time chunks so that the grid fills the
 // chip (the two-pass scheme whose carry step the reference left as TODO at
@@ -31,15 +34,15 @@ namespace mvm {
 enum FwdMode { kAgg = 0, kMain = 1 };
 
 template <typename XT, typename OT, int MODE>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 6)
 scan_fwd_kernel(Geom gm, FwdBufs bf) {
-  // double-buffered tile staging: u, delta (64 channels), B, C (16 states),
-  // and y (written back coalesced one tile later)
+  // double-buffered tile staging: u, delta (64 channels), B, C (16 states);
+  // y replaces u in place and is written back coalesced one tile later (each
+  // thread flushes exactly the LDS slots it refills with the next prefetch)
   __shared__ float sU[2][kSub][kChPerBlock];
   __shared__ float sD[2][kSub][kChPerBlock];
   __shared__ float sB[2][kSub][kStatePad];
   __shared__ float sC[2][kSub][kStatePad];
-  __shared__ float sY[2][kSub][kChPerBlock];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -95,7 +98,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       const int tt = wrow + 4 * r;
       if (tt < nt) {
         OT* rowp = y + (xrow + token_row(tok, ts + tt, gm.L) * gm.xst + ch0);
-        if (dld < gm.D) st(rowp, lch, sY[buf][tt][lch]);
+        if (dld < gm.D) st(rowp, lch, sU[buf][tt][lch]);
       }
     }
   };
@@ -121,7 +124,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     if (MODE == kAgg) dsum += dl;
     if (MODE == kMain) {  // the channel's 4 lanes store the same y (no branch)
       yp = sum_groups(yp);
-      sY[buf][tt][cl] = fmaf(dskip, uu, yp);
+      sU[buf][tt][cl] = fmaf(dskip, uu, yp);  // in place: u_t is consumed
     }
   };
   auto store_ck = [&](int64_t pos_end) {  // state after position pos_end (== 8s + 7)
