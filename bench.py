@@ -2,6 +2,7 @@
 scan's fwd+VJP bandwidth, printed as one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --scan-driver     (profiling driver, see scan_driver)
 
 Workload (the step timed): VisionMamba encoder, 2D, K=4 scan directions,
 batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
@@ -16,7 +17,10 @@ roofline: the selective-scan backward call (the largest hand-written piece
 of the step; its kernels are listed in "kernel"), timed with HIP events on
 the stream it runs on for every launch inside the timed region; achieved =
 algorithmic bytes per launch / mean launch time, against the MI355X HBM3E
-peak of 8 TB/s.
+peak of 8 TB/s.  traffic = HBM bytes per backward call at this shape from
+the rocprofv3 FETCH_SIZE and WRITE_SIZE counters, each scaled by what it
+reads for a 512 MiB copy (committed summary in profiles/, made with
+`bench.py --scan-driver`), or null when that summary is absent.
 
 scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
 D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads.
@@ -120,6 +124,58 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
     }
 
 
+def step_scan_inputs(torch, device):
+    """The scan call of one VisionMamba-2D layer of the step: B=32, K=4
+    directions of a 14x14 grid (L=196), D=768, N=16, fp32, B and C as
+    strided column slices of a (B, L, K, 24 + 2N) projection output."""
+    from mlx_vision_mamba_amd import directions
+    bsz, L, K, D, N = 32, 196, 4, 768, 16
+    g = torch.Generator().manual_seed(0)
+    u = torch.randn(bsz, L, K, D, generator=g).to(device)
+    dl = torch.nn.functional.softplus(torch.randn(bsz, L, K, D, generator=g) * 0.5 - 4.6).to(device)
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(K, D, 1).to(device)
+    dbc = torch.randn(bsz, L, K, 24 + 2 * N, generator=g).to(device)
+    Bm, Cm = dbc[..., 24:24 + N], dbc[..., 24 + N:]
+    Dv = torch.ones(K, D, device=device)
+    dy = torch.randn(bsz, L, K, D, generator=g).to(device)
+    tok = directions.seq_to_tok_table(K, L, (14, 14)).to(device)
+    return (u, dl, A, Bm, Cm, Dv), dy, tok
+
+
+def scan_driver(torch, scan, device):
+    """Profiling driver (--scan-driver): one 512 MiB device copy, whose HBM
+    traffic is known and calibrates the byte counters, then two scan
+    forward + VJP calls at the VisionMamba step shape."""
+    src = torch.empty(128 * 1024 * 1024, dtype=torch.float32, device=device).uniform_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    args, dy, tok = step_scan_inputs(torch, device)
+    for _ in range(2):
+        y, ck = scan.scan_forward(*args, tok, save_ckpt=True)
+        scan.scan_backward(*args, dy, ckpt=ck, tok=tok)
+    torch.cuda.synchronize()
+    print(json.dumps({"scan_driver": "done", "shape": "B=32 L=196 K=4 D=768 N=16 fp32"}), flush=True)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")
+
+
+def measured_traffic(key):
+    """HBM bytes per call measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on
+    the scan at the VisionMamba step shape (a line `key: <bytes>` of the
+    committed profile summary), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return int(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(torch):
     """Oracle VisionMamba step on the host cores: batch 2, one step."""
     from oracle import torch_ref
@@ -143,11 +199,36 @@ def cpu_baseline(torch):
     t0 = time.perf_counter()
     step()
     dt = time.perf_counter() - t0
+    scan_cpu = cpu_scan_baseline(torch)
     return {"value": round(2 / dt, 3), "unit": "imgs/s", "cores": cores, "kind": "port",
             "sample": "VisionMamba-2D K=4 step (fwd + mean loss + bwd), batch 2 of the same "
                       "224x224x1 / patch 16 / E=384 / depth 6 model, float32, reference's "
                       "sequential scan restated in torch; 1 warm-up + 1 timed step",
-            "seconds_per_step": round(dt, 2)}
+            "seconds_per_step": round(dt, 2), "scan": scan_cpu}
+
+
+def cpu_scan_baseline(torch):
+    """The reference's sequential and chunked scans (restated in torch,
+    materialised discretisation, per-step loop) forward + VJP on the host at
+    B=2, L=196, D=1536, N=16 fp32: 1 warm-up, median of 5."""
+    from oracle import torch_ref
+    from tests import scan_inputs
+    from mlx_vision_mamba_amd.scan import algorithmic_bytes
+    u, dl, A, Bm, Cm, Dv, g = scan_inputs.make(2, 196, 1536, 16, seed=0)
+    nbytes = sum(algorithmic_bytes(2, 196, 1536, 16, 4, 4))
+    out = {}
+    for name, fn in (("sequential", torch_ref.scan_sequential), ("chunked", torch_ref.scan_chunked)):
+        times = []
+        for _ in range(6):
+            ins = [t.clone().requires_grad_(True) for t in (u, dl, A, Bm, Cm, Dv)]
+            t0 = time.perf_counter()
+            y = fn(*ins)
+            torch.autograd.grad(y, ins, g)
+            times.append(time.perf_counter() - t0)
+        med = sorted(times[1:])[2]
+        out[name] = {"fwd_vjp_ms": round(med * 1e3, 2), "GBps": round(nbytes / med / 1e9, 3)}
+    out["shape"] = "B=2 L=196 D=1536 N=16 fp32"
+    return out
 
 
 def main():
@@ -156,6 +237,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--scan-driver", action="store_true",
+                    help="profiling driver only: a 512 MiB copy + 2 scan fwd/VJP calls at the "
+                         "VisionMamba step shape")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the selective-scan path is benchmarked on a "
@@ -168,6 +252,9 @@ def main():
     from mlx_vision_mamba_amd import scan
 
     device = torch.device("cuda:0")
+    if args.scan_driver:
+        scan_driver(torch, scan, device)
+        return
     elapsed, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
     imgs = 32 * args.steps / elapsed
 
@@ -180,7 +267,8 @@ def main():
     achieved = bwd_b / bwd_t / 1e9
     roofline = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": measured_traffic("bwd_call_hbm_bytes"),
         "kernel": BWD_KERNELS,
         "algorithmic_bytes_per_launch": int(bwd_b), "avg_launch_us": round(bwd_t * 1e6, 2),
         "launches": len(bwd),
