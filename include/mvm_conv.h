@@ -16,8 +16,10 @@
  * Conventions are those of mvm_scan.h (status codes, mvm_last_error,
  * caller-owned buffers, host-side validation, deterministic results).
  * float32 only.  Layout: x holds (b, k, t, d) at
- * b*x_stride_b + k*x_stride_k + t*x_stride_t + d; y, dy and dx use the
- * y_stride_* strides; w is (ndir, dim, kwidth) and bias (ndir, dim).
+ * b*x_stride_b + k*x_stride_k + t*x_stride_t + d; y and dy use the
+ * y_stride_* strides, dx the dx_stride_* strides (so dx can be written
+ * straight into a slice of a larger gradient buffer); w is
+ * (ndir, dim, kwidth) and bias (ndir, dim).
  */
 #ifndef MVM_CONV_H
 #define MVM_CONV_H
@@ -40,6 +42,7 @@ typedef struct mvm_conv_desc {
   int64_t x_stride_b, x_stride_k, x_stride_t;
   int64_t y_stride_b, y_stride_k, y_stride_t;
   const int32_t* seq_to_tok; /* device (ndir, seqlen) table or NULL */
+  int64_t dx_stride_b, dx_stride_k, dx_stride_t;
 } mvm_conv_desc;
 
 /* Validates a descriptor without touching the GPU. */
@@ -52,7 +55,7 @@ int64_t mvm_conv_workspace_bytes(const mvm_conv_desc* desc);
 int mvm_conv_silu_fwd(const mvm_conv_desc* desc, const float* x, const float* w,
                       const float* bias, float* y, void* stream);
 
-/* Gradients of mvm_conv_silu_fwd for upstream dy: dx (y layout), dw
+/* Gradients of mvm_conv_silu_fwd for upstream dy: dx (dx_stride_*), dw
  * (ndir, dim, kwidth), dbias (ndir, dim); all fully written. */
 int mvm_conv_silu_bwd(const mvm_conv_desc* desc, const float* x, const float* w,
                       const float* bias, const float* dy, float* dx, float* dw,

@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define MVM_ABI_VERSION 1
+#define MVM_ABI_VERSION 2
 
 /* status codes */
 #define MVM_OK 0
@@ -125,6 +125,63 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta,
                  const float* Dv, const float* ckpt, const void* dy, void* du,
                  float* ddelta, float* dA, void* dB, void* dC, float* dD,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused form: the Mamba block's prologue and epilogue around the scan.
+ *
+ * Replaces, for one block call, the ops around scan_fn in MambaBlock
+ * (mlx_vision_mamba/mamba_block.py:180-190):
+ *     delta = softplus(dt_proj(dt))          (:180-181; dt_proj's bias is
+ *                                             delta_bias, its matmul output
+ *                                             is delta_raw)
+ *     y     = scan_fn(x, delta, A, B, C, D)  (:187)
+ *     y     = y * silu(z)                    (:190)
+ * plus their VJP.  softplus is applied inside the scan kernels as delta is
+ * staged (forward and backward), and the gate as y is written back, so
+ * neither makes its own pass over HBM; the gate's backward is one coalesced
+ * pointwise pass ahead of the backward scan.  float32 only
+ * (in_dtype = out_dtype = MVM_F32).
+ *
+ * Layouts: `scan` gives the sizes, u / du strides (x_stride_*), the B-like
+ * strides and the direction table.  delta_raw / ddelta_raw use dt_stride_*,
+ * y / y_raw / dy use y_stride_*, z / dz use z_stride_* (all with channel
+ * stride 1).  softplus(x) = x for x > 20, else log(1 + e^x) (torch's
+ * threshold); silu(z) = z / (1 + e^-z).
+ * ---------------------------------------------------------------------- */
+typedef struct mvm_scan_fused_desc {
+  mvm_scan_desc scan;
+  int64_t dt_stride_b, dt_stride_k, dt_stride_t;  /* delta_raw, ddelta_raw */
+  int64_t y_stride_b, y_stride_k, y_stride_t;     /* y, y_raw, dy */
+  int64_t z_stride_b, z_stride_k, z_stride_t;     /* z, dz */
+} mvm_scan_fused_desc;
+
+int mvm_scan_fused_validate(const mvm_scan_fused_desc* desc);
+
+/* Workspace bytes of mvm_scan_fused_fwd (which = 0) or mvm_scan_fused_bwd
+ * (which = 1); gate != 0 when z is given.  Checkpoints are sized by
+ * mvm_scan_ckpt_elems(&desc->scan). */
+int64_t mvm_scan_fused_workspace_bytes(const mvm_scan_fused_desc* desc, int which, int gate);
+
+/* y = scan(u, softplus(delta_raw + delta_bias), A, Bm, Cm, Dv) * silu(z).
+ * delta_bias (ndir, dim) may be NULL (zero bias); z may be NULL (no gate,
+ * y is the scan output).  y_raw (the ungated scan output, needed by the
+ * backward when z is given) and ckpt (training) may be NULL. */
+int mvm_scan_fused_fwd(const mvm_scan_fused_desc* desc, const float* u, const float* delta_raw,
+                       const float* delta_bias, const float* A, const float* Bm,
+                       const float* Cm, const float* Dv, const float* z, float* y,
+                       float* y_raw, float* ckpt, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* VJP of mvm_scan_fused_fwd for upstream dy (gradient of the gated y).
+ * ckpt is required; y_raw and dz are required when z is given; ddelta_bias
+ * (ndir, dim) is required when delta_bias is given.  ddelta_raw is the
+ * gradient of delta_raw; every output is fully written. */
+int mvm_scan_fused_bwd(const mvm_scan_fused_desc* desc, const float* u, const float* delta_raw,
+                       const float* delta_bias, const float* A, const float* Bm,
+                       const float* Cm, const float* Dv, const float* z, const float* y_raw,
+                       const float* ckpt, const float* dy, float* du, float* ddelta_raw,
+                       float* ddelta_bias, float* dA, float* dB, float* dC, float* dD,
+                       float* dz, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ MVM_ERR_HIP = -4
 MVM_F32 = 0
 MVM_BF16 = 1
 MVM_MAX_DSTATE = 16
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -43,6 +43,17 @@ class ScanDesc(ctypes.Structure):
     ]
 
 
+class FusedDesc(ctypes.Structure):
+    """Mirror of ``mvm_scan_fused_desc`` (include/mvm_scan.h)."""
+
+    _fields_ = [
+        ("scan", ScanDesc),
+        ("dt_stride_b", _i64), ("dt_stride_k", _i64), ("dt_stride_t", _i64),
+        ("y_stride_b", _i64), ("y_stride_k", _i64), ("y_stride_t", _i64),
+        ("z_stride_b", _i64), ("z_stride_k", _i64), ("z_stride_t", _i64),
+    ]
+
+
 class ConvDesc(ctypes.Structure):
     """Mirror of ``mvm_conv_desc`` (include/mvm_conv.h)."""
 
@@ -51,6 +62,7 @@ class ConvDesc(ctypes.Structure):
         ("x_stride_b", _i64), ("x_stride_k", _i64), ("x_stride_t", _i64),
         ("y_stride_b", _i64), ("y_stride_k", _i64), ("y_stride_t", _i64),
         ("seq_to_tok", _vp),
+        ("dx_stride_b", _i64), ("dx_stride_k", _i64), ("dx_stride_t", _i64),
     ]
 
 
@@ -65,6 +77,10 @@ SIGNATURES = {
     "mvm_scan_chunk_len": (_i64, [ctypes.POINTER(ScanDesc)]),
     "mvm_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 9 + [ctypes.c_size_t, _vp]),
     "mvm_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 15 + [ctypes.c_size_t, _vp]),
+    "mvm_scan_fused_validate": (ctypes.c_int, [ctypes.POINTER(FusedDesc)]),
+    "mvm_scan_fused_workspace_bytes": (_i64, [ctypes.POINTER(FusedDesc), ctypes.c_int, ctypes.c_int]),
+    "mvm_scan_fused_fwd": (ctypes.c_int, [ctypes.POINTER(FusedDesc)] + [_vp] * 12 + [ctypes.c_size_t, _vp]),
+    "mvm_scan_fused_bwd": (ctypes.c_int, [ctypes.POINTER(FusedDesc)] + [_vp] * 20 + [ctypes.c_size_t, _vp]),
     "mvm_conv_validate": (ctypes.c_int, [ctypes.POINTER(ConvDesc)]),
     "mvm_conv_workspace_bytes": (_i64, [ctypes.POINTER(ConvDesc)]),
     "mvm_conv_silu_fwd": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [_vp] * 5),

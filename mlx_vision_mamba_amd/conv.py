@@ -16,14 +16,45 @@ from . import _lib
 from .scan import _check_device, _ptr, _stream_ptr
 
 
-def _desc(x, y_strides, kc, tok):
+def _desc(x, y_strides, kc, tok, dx_strides=None):
+    """Conv descriptor; strides are given in (b, t, k) order of a (B, N, K, D)
+    view.  dx uses y's strides unless given."""
     bsz, L, K, D = x.shape
     d = _lib.ConvDesc()
     d.batch, d.seqlen, d.dim, d.ndir, d.kwidth = bsz, L, D, K, kc
     d.x_stride_b, d.x_stride_t, d.x_stride_k = x.stride(0), x.stride(1), x.stride(2)
     d.y_stride_b, d.y_stride_t, d.y_stride_k = y_strides[0], y_strides[1], y_strides[2]
+    dxs = dx_strides if dx_strides is not None else y_strides
+    d.dx_stride_b, d.dx_stride_t, d.dx_stride_k = dxs[0], dxs[1], dxs[2]
     d.seq_to_tok = tok.data_ptr() if tok is not None else None
     return d
+
+
+def conv_silu_forward_into(x, w, b, y, tok):
+    """Raw forward launch: y (a (B, N, K, D) view with channel stride 1, any
+    other strides) = silu(conv(x) + b) along each direction's scan order."""
+    K, D, kc = w.shape
+    desc = _desc(x, y.stride(), kc, tok)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().mvm_conv_silu_fwd(ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(b),
+                                                _ptr(y), ctypes.c_void_p(_stream_ptr(x.device))))
+
+
+def conv_silu_backward_into(x, w, b, dy, dx, tok):
+    """Raw backward launch: writes dx (a view with its own strides, e.g. a
+    slice of a larger gradient buffer) and returns (dw, dbias)."""
+    K, D, kc = w.shape
+    dw = torch.empty_like(w)
+    db = torch.empty_like(b)
+    desc = _desc(x, dy.stride(), kc, tok, dx.stride())
+    lib = _lib.lib()
+    with torch.cuda.device(x.device):
+        nbytes = _lib.check(lib.mvm_conv_workspace_bytes(ctypes.byref(desc)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        _lib.check(lib.mvm_conv_silu_bwd(ctypes.byref(desc), _ptr(x), _ptr(w), _ptr(b), _ptr(dy),
+                                         _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws), nbytes,
+                                         ctypes.c_void_p(_stream_ptr(x.device))))
+    return dw, db
 
 
 class _ConvSiluFn(torch.autograd.Function):

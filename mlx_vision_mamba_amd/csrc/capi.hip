@@ -99,6 +99,11 @@ mvm::Geom make_geom(const mvm_scan_desc* d) {
   g.xsb = d->x_stride_b;
   g.xsk = d->x_stride_k;
   g.xst = d->x_stride_t;
+  // the plain scan's delta / ddelta and y / dy share u's layout
+  g.dsb = g.ysb = d->x_stride_b;
+  g.dsk = g.ysk = d->x_stride_k;
+  g.dst = g.yst = d->x_stride_t;
+  g.zsb = g.zsk = g.zst = 0;
   g.bsb = d->bc_stride_b;
   g.bsk = d->bc_stride_k;
   g.bst = d->bc_stride_t;
@@ -286,6 +291,163 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta, c
 
 }  // extern "C"
 
+// ----------------------------------------------------------- fused form
+
+namespace {
+
+int check_fused(const mvm_scan_fused_desc* fd) {
+  if (fd == nullptr) return fail(MVM_ERR_INVALID_ARG, "fused desc is NULL");
+  const int rc = check_desc(&fd->scan);
+  if (rc != MVM_OK) return rc;
+  if (fd->scan.in_dtype != MVM_F32 || fd->scan.out_dtype != MVM_F32)
+    return fail(MVM_ERR_UNSUPPORTED, "the fused scan is float32 only");
+  const int64_t st[9] = {fd->dt_stride_b, fd->dt_stride_k, fd->dt_stride_t,
+                         fd->y_stride_b, fd->y_stride_k, fd->y_stride_t,
+                         fd->z_stride_b, fd->z_stride_k, fd->z_stride_t};
+  for (int64_t v : st)
+    if (v < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride in fused desc");
+  const int64_t dim = fd->scan.dim;
+  if (fd->scan.seqlen > 1 &&
+      (fd->dt_stride_t < dim || fd->y_stride_t < dim || (fd->z_stride_t != 0 && fd->z_stride_t < dim)))
+    return fail(MVM_ERR_INVALID_ARG, "fused row stride overlaps channels (dim=%lld)", (long long)dim);
+  if (fd->scan.batch * fd->scan.ndir * fd->scan.seqlen > INT32_MAX)
+    return fail(MVM_ERR_UNSUPPORTED, "batch*ndir*seqlen exceeds 2^31-1");
+  return MVM_OK;
+}
+
+mvm::Geom fused_geom(const mvm_scan_fused_desc* fd) {
+  mvm::Geom g = make_geom(&fd->scan);
+  g.dsb = fd->dt_stride_b; g.dsk = fd->dt_stride_k; g.dst = fd->dt_stride_t;
+  g.ysb = fd->y_stride_b;  g.ysk = fd->y_stride_k;  g.yst = fd->y_stride_t;
+  g.zsb = fd->z_stride_b;  g.zsk = fd->z_stride_k;  g.zst = fd->z_stride_t;
+  return g;
+}
+
+// fused backward workspace: the plain backward's pieces and the dt_bias
+// partials (the gate needs none: it is undone in the scan's staging)
+struct FusedBwdWs {
+  BwdWs base;
+  size_t part_db = 0, total = 0;
+};
+FusedBwdWs fused_bwd_ws(const mvm::Geom& g) {
+  FusedBwdWs w;
+  w.base = bwd_ws(g, false);
+  w.part_db = align_up(static_cast<size_t>(g.B * g.K * g.nchunk * g.D) * sizeof(double));
+  w.total = w.base.total + w.part_db;
+  return w;
+}
+
+int check_ws(const char* who, void* ws, size_t have, size_t need) {
+  if (have < need) return fail(MVM_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", who, have, need);
+  if (need > 0 && ws == nullptr) return fail(MVM_ERR_WORKSPACE, "%s: workspace is NULL", who);
+  if ((reinterpret_cast<uintptr_t>(ws) & (kAlign - 1)) != 0)
+    return fail(MVM_ERR_WORKSPACE, "%s: workspace must be %zu-byte aligned", who, kAlign);
+  return MVM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvm_scan_fused_validate(const mvm_scan_fused_desc* desc) {
+  const int rc = check_fused(desc);
+  return rc == MVM_OK ? ok() : rc;
+}
+
+int64_t mvm_scan_fused_workspace_bytes(const mvm_scan_fused_desc* desc, int which, int gate) {
+  const int rc = check_fused(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = fused_geom(desc);
+  if (which == 0) return static_cast<int64_t>(fwd_ws(g).total);
+  (void)gate;  // the gate adds no workspace
+  if (which == 1) return static_cast<int64_t>(fused_bwd_ws(g).total);
+  return fail(MVM_ERR_INVALID_ARG, "which=%d must be 0 or 1", which);
+}
+
+int mvm_scan_fused_fwd(const mvm_scan_fused_desc* desc, const float* u, const float* delta_raw,
+                       const float* delta_bias, const float* A, const float* Bm, const float* Cm,
+                       const float* Dv, const float* z, float* y, float* y_raw, float* ckpt,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_fused(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = fused_geom(desc);
+  const bool empty = g.B == 0 || g.L == 0 || g.D == 0;
+  if (!empty) {
+    if (!u || !delta_raw || !A || !Bm || !Cm || !Dv || !y)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_fwd: NULL input or y pointer");
+    if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_fwd: ckpt must be 16-byte aligned");
+  }
+  const FwdWs w = fwd_ws(g);
+  rc = check_ws("mvm_scan_fused_fwd", workspace, workspace_bytes, w.total);
+  if (rc != MVM_OK) return rc;
+  if (empty) return ok();
+  char* ws = static_cast<char*>(workspace);
+  mvm::FwdBufs b{u, delta_raw, A, Bm, Cm, Dv, y, ckpt,
+                 reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + w.agg_h),
+                 delta_bias, z, y_raw};
+  return hip_status(mvm::launch_fused_fwd(g, b, static_cast<hipStream_t>(stream)),
+                    "mvm_scan_fused_fwd launch");
+}
+
+int mvm_scan_fused_bwd(const mvm_scan_fused_desc* desc, const float* u, const float* delta_raw,
+                       const float* delta_bias, const float* A, const float* Bm, const float* Cm,
+                       const float* Dv, const float* z, const float* y_raw, const float* ckpt,
+                       const float* dy, float* du, float* ddelta_raw, float* ddelta_bias,
+                       float* dA, float* dB, float* dC, float* dD, float* dz, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  int rc = check_fused(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = fused_geom(desc);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool empty = g.B == 0 || g.L == 0 || g.D == 0;
+  const bool gate = z != nullptr;
+  if (g.D > 0 && (!dA || !dD)) return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: NULL dA or dD");
+  if (g.D > 0 && delta_bias && !ddelta_bias)
+    return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: delta_bias given but ddelta_bias is NULL");
+  if (!empty) {
+    if (!u || !delta_raw || !A || !Bm || !Cm || !Dv || !dy || !ckpt)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: NULL input pointer (ckpt is required)");
+    if (!du || !ddelta_raw || !dB || !dC)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: NULL output pointer");
+    if (gate && (!y_raw || !dz))
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: a gate needs y_raw and dz");
+    if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: ckpt must be 16-byte aligned");
+  }
+  const FusedBwdWs w = fused_bwd_ws(g);
+  if (!empty) {
+    rc = check_ws("mvm_scan_fused_bwd", workspace, workspace_bytes, w.total);
+    if (rc != MVM_OK) return rc;
+  }
+  if (empty) {
+    hipError_t e = mvm::launch_fill(dA, g.K * g.D * g.N, 0.f, s);
+    if (e == hipSuccess) e = mvm::launch_fill(dD, g.K * g.D, 0.f, s);
+    if (e == hipSuccess && ddelta_bias) e = mvm::launch_fill(ddelta_bias, g.K * g.D, 0.f, s);
+    return hip_status(e, "mvm_scan_fused_bwd fill");
+  }
+  char* ws = static_cast<char*>(workspace);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = ws + off;
+    off += bytes;
+    return bytes ? p : nullptr;
+  };
+  float* agg_mu = reinterpret_cast<float*>(take(w.base.agg_mu));
+  float* agg_s = reinterpret_cast<float*>(take(w.base.agg_s));
+  double* part_dA = reinterpret_cast<double*>(take(w.base.part_dA));
+  double* part_dD = reinterpret_cast<double*>(take(w.base.part_dD));
+  float* part_bc = reinterpret_cast<float*>(take(w.base.part_bc));
+  double* part_db = reinterpret_cast<double*>(take(w.part_db));
+  mvm::BwdBufs b{u, delta_raw, A, Bm, Cm, Dv, ckpt, dy, du, ddelta_raw, dA, dB, dC, dD,
+                 agg_mu, agg_s, part_dA, part_dD, part_bc, delta_bias,
+                 delta_bias ? ddelta_bias : nullptr, part_db,
+                 gate ? z : nullptr, gate ? y_raw : nullptr, gate ? dz : nullptr};
+  return hip_status(mvm::launch_fused_bwd(g, b, s), "mvm_scan_fused_bwd launch");
+}
+
+}  // extern "C"
+
 namespace {
 
 int check_conv(const mvm_conv_desc* d) {
@@ -296,11 +458,12 @@ int check_conv(const mvm_conv_desc* d) {
   if (d->kwidth < 1 || d->kwidth > MVM_CONV_MAX_KWIDTH)
     return fail(MVM_ERR_UNSUPPORTED, "kwidth=%lld unsupported (1..%d)", (long long)d->kwidth,
                 MVM_CONV_MAX_KWIDTH);
-  const int64_t st[6] = {d->x_stride_b, d->x_stride_k, d->x_stride_t,
-                         d->y_stride_b, d->y_stride_k, d->y_stride_t};
+  const int64_t st[9] = {d->x_stride_b, d->x_stride_k, d->x_stride_t,
+                         d->y_stride_b, d->y_stride_k, d->y_stride_t,
+                         d->dx_stride_b, d->dx_stride_k, d->dx_stride_t};
   for (int64_t v : st)
     if (v < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride in conv desc");
-  if (d->seqlen > 1 && (d->x_stride_t < d->dim || d->y_stride_t < d->dim))
+  if (d->seqlen > 1 && (d->x_stride_t < d->dim || d->y_stride_t < d->dim || d->dx_stride_t < d->dim))
     return fail(MVM_ERR_INVALID_ARG, "conv row stride overlaps channels");
   if (d->batch * d->ndir > 65535) return fail(MVM_ERR_UNSUPPORTED, "batch*ndir exceeds 65535");
   return MVM_OK;
@@ -311,6 +474,7 @@ mvm::ConvGeom conv_geom(const mvm_conv_desc* d) {
   g.B = d->batch; g.L = d->seqlen; g.D = d->dim; g.K = d->ndir;
   g.xsb = d->x_stride_b; g.xsk = d->x_stride_k; g.xst = d->x_stride_t;
   g.ysb = d->y_stride_b; g.ysk = d->y_stride_k; g.yst = d->y_stride_t;
+  g.dxsb = d->dx_stride_b; g.dxsk = d->dx_stride_k; g.dxst = d->dx_stride_t;
   g.tok = d->seq_to_tok;
   return g;
 }

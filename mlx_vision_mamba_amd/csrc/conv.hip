@@ -85,6 +85,7 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
   const int32_t* tok = g.tok ? g.tok + k * g.L : nullptr;
   const int64_t xb = b * g.xsb + k * g.xsk;
   const int64_t yb = b * g.ysb + k * g.ysk;
+  const int64_t dxb = b * g.dxsb + k * g.dxsk;
   float wv[KC];
 #pragma unroll
   for (int j = 0; j < KC; ++j) wv[j] = dvalid ? w[(k * g.D + d) * KC + j] : 0.f;
@@ -121,7 +122,7 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < KC; ++j) acc = fmaf(wv[j], gp[i + (KC - 1) - j], acc);
-    if (dvalid && p < g.L) dx[yb + token_row(tok, p, g.L) * g.yst + d] = acc;
+    if (dvalid && p < g.L) dx[dxb + token_row(tok, p, g.L) * g.dxst + d] = acc;
     // dw[j] += dpre[p] * x[p - (KC-1) + j]; db += dpre[p]
 #pragma unroll
     for (int j = 0; j < KC; ++j) dwp[j] = fmaf(gp[i], xw[i + j], dwp[j]);

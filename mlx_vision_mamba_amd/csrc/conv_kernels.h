@@ -10,7 +10,8 @@ namespace mvm {
 struct ConvGeom {
   int64_t B, L, D, K;
   int64_t xsb, xsk, xst;   // input strides (channel stride 1)
-  int64_t ysb, ysk, yst;   // output / dy / dx strides (channel stride 1)
+  int64_t ysb, ysk, yst;   // output / dy strides (channel stride 1)
+  int64_t dxsb, dxsk, dxst;  // dx strides (channel stride 1)
   const int32_t* tok;      // (K, L) scan position -> token row, or nullptr
 };
 

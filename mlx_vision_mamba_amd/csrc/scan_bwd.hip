@@ -30,6 +30,15 @@
 //            partials per (b, chunk), summed in float64 by reduce_ad_kernel.
 // Long sequences: the adjoint carry between time chunks uses the same
 // two-pass idea as the forward, run right to left (bwd_agg + bwd_carry).
+//
+// Fused form (FUSE, float32): delta = softplus(delta_raw + dt_bias) is
+// applied as the delta tile is staged; the stored gradient is that of
+// delta_raw, ddelta * sigmoid(delta_raw + dt_bias), with sigmoid recovered
+// from the staged delta as 1 - exp(-delta); dt_bias's gradient is its sum
+// over (b, t), reduced like dD.  The gate y = y_raw * silu(z) is undone as
+// the upstream gradient is staged: the scan consumes g = dy * silu(z), and
+// dz = dy * y_raw * silu'(z) is written from the same registers, so the
+// gate's backward makes no pass of its own.
 #include <type_traits>
 
 #include "scan_common.h"
@@ -39,7 +48,7 @@ namespace mvm {
 
 // Pass 1: adjoint aggregate of chunks 1..nchunk-1: the mu that leaves the
 // chunk's first position when mu = 0 enters its last, and sum(delta).
-template <typename XT>
+template <typename XT, bool FUSE>
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   __shared__ float sD[2][kSub][kChPerBlock];
@@ -61,10 +70,28 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xrow = b * gm.xsb + k * gm.xsk;
+  const int64_t drow = b * gm.dsb + k * gm.dsk;
+  const int64_t yrow = b * gm.ysb + k * gm.ysk;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
   const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
   const XT* __restrict__ dy = static_cast<const XT*>(bf.dy);
+  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  auto stage_delta = [&](float (&v)[4]) {
+    if (FUSE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = softplus_f(v[r] + dbias_l);
+    }
+  };
+  // fused gate: the scan's upstream gradient is dy * silu(z)
+  const int64_t zrow = b * gm.zsb + k * gm.zsk;
+  const bool gate = FUSE && bf.z != nullptr;
+  float pz[4] = {0.f, 0.f, 0.f, 0.f};
+  auto stage_g = [&](float (&gv)[4]) {
+    if (gate) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) gv[r] *= pz[r] * sigmoid_f(pz[r]);
+    }
+  };
 
   float a2[4], mu[4];
 #pragma unroll
@@ -79,9 +106,12 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   {
     const int64_t ts = t0 + (ntile - 1) * kSub;
     const int nt = static_cast<int>(t1 - ts);
-    load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
-    load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, ts, nt, gm.L, tid);
+    load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
+    if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
     pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+    stage_delta(pd);
+    stage_g(pg);
     store_xtile(sD[0], pd, tid);
     store_xtile(sG[0], pg, tid);
     sC[0][tid >> 4][tid & 15] = pc;
@@ -94,8 +124,9 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
     const bool more = j + 1 < ntile;
     if (more) {
       const int64_t tn = ts - kSub;
-      load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
+      if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, tn, kSub, gm.L, tid);
       pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
     }
 #pragma unroll
@@ -114,6 +145,8 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
       }
     }
     if (more) {
+      stage_delta(pd);
+      stage_g(pg);
       store_xtile(sD[buf ^ 1], pd, tid);
       store_xtile(sG[buf ^ 1], pg, tid);
       sC[buf ^ 1][tid >> 4][tid & 15] = pc;
@@ -155,18 +188,19 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
 // Pass 3: the reverse sweep.  Each 16-step tile is processed as two 8-step
 // halves (later half first), each restarted from its checkpoint, so the
 // register tile is 9 x 4 states + 8 x 4 decays and three waves fit per SIMD.
-template <typename XT, typename OT>
+template <typename XT, typename OT, bool FUSE>
 __global__ void __launch_bounds__(kThreads, 2)
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
-  // written in place over u / delta of the same step once it is consumed;
-  // per-wave channel sums of dB | dC
+  // written in place over u / dy of the same step once it is consumed (delta
+  // stays for the fused softplus gradient); per-wave channel sums of dB | dC
   __shared__ float sU[2][kSub][kChPerBlock];
   __shared__ float sD[2][kSub][kChPerBlock];
   __shared__ float sG[2][kSub][kChPerBlock];
   __shared__ float sB[2][kSub][kStatePad];
   __shared__ float sC[2][kSub][kStatePad];
   __shared__ float sRed[2][4][kSub][2][kStatePad];
+  __shared__ double sDb[4][kChPerBlock];  // fused: per-wave dt_bias gradient sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -186,6 +220,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
   const int64_t xrow = b * gm.xsb + k * gm.xsk;
+  const int64_t drow = b * gm.dsb + k * gm.dsk;
+  const int64_t yrow = b * gm.ysb + k * gm.ysk;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -222,21 +258,57 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     if (p > 0 && dvalid) h4 = *reinterpret_cast<const float4*>(ckb + (p / kCk - 1) * ck_stride);
     return h4;
   };
+  // fused: the dt bias of the channel this thread stages / flushes, and its
+  // gradient summed over the rows this thread flushes
+  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  double dbacc = 0.0;
+  auto stage_delta = [&](float (&v)[4]) {
+    if (FUSE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = softplus_f(v[r] + dbias_l);
+    }
+  };
+  // fused gate: the upstream dy is the gradient of y_raw * silu(z); the scan
+  // consumes g = dy * silu(z) and dz = dy * y_raw * silu'(z) leaves from the
+  // staging registers of the tile (rows ts + tt, tt = wave + 4r)
+  const int64_t zrow = b * gm.zsb + k * gm.zsk;
+  const bool gate = FUSE && bf.z != nullptr;
+  float pz[4] = {0.f, 0.f, 0.f, 0.f}, pyr[4] = {0.f, 0.f, 0.f, 0.f};
+  auto stage_gate = [&](float (&gv)[4], int64_t ts, int nt) {
+    if (gate) {
+      const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sg = sigmoid_f(pz[r]);
+        const float dzv = gv[r] * pyr[r] * (sg * fmaf(pz[r], 1.f - sg, 1.f));
+        gv[r] *= pz[r] * sg;
+        const int tt = wrow + 4 * r;
+        if (tt < nt && dld < gm.D) bf.dz[zrow + token_row(tok, ts + tt, gm.L) * gm.zst + dld] = dzv;
+      }
+    }
+  };
   // write back du / ddelta rows and this block's dB | dC partials of a tile
   auto flush = [&](int buf, int64_t ts, int nt) {
     const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lch = tid & 63;
+    float dbt = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
       if (tt < nt) {
-        const int64_t off = xrow + token_row(tok, ts + tt, gm.L) * gm.xst + ch0;
+        const int64_t row = token_row(tok, ts + tt, gm.L);
         if (dld < gm.D) {
-          st(du_out + off, lch, sU[buf][tt][lch]);
-          bf.ddelta[off + lch] = sD[buf][tt][lch];
+          st(du_out + (xrow + row * gm.xst + ch0), lch, sU[buf][tt][lch]);
+          float dd = sG[buf][tt][lch];
+          if (FUSE) {
+            dd *= softplus_grad_from_value(sD[buf][tt][lch]);
+            dbt += dd;
+          }
+          bf.ddelta[drow + row * gm.dst + dld] = dd;
         }
       }
     }
+    if (FUSE) dbacc += static_cast<double>(dbt);
     float* pbc = bf.part_bc + ((bk * gm.ncblk + blockIdx.x) * gm.L + ts) * (2 * kStatePad);
     for (int i = tid; i < nt * 2 * kStatePad; i += kThreads) {
       const int tt = i / (2 * kStatePad);
@@ -298,10 +370,10 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         sa = sum_groups(sa);
         sb = sum_groups(sb);
         tD = fmaf(gy, uu, tD);
-        // in place: this step's u / delta are consumed (the 4 lanes of the
+        // in place: this step's u / dy are consumed (the 4 lanes of the
         // channel store the same values)
         sU[buf][tt][cl] = fmaf(dl, sb, dskip * gy);
-        sD[buf][tt][cl] = fmaf(uu, sb, sa);
+        sG[buf][tt][cl] = fmaf(uu, sb, sa);
         const float rb = channel_reduce4(xb[0], xb[1], xb[2], xb[3]);
         const float rc = channel_reduce4(xc[0], xc[1], xc[2], xc[3]);
         // lanes with equal (g, j) hold equal sums and store them together
@@ -318,12 +390,18 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     const int64_t ts = t0 + (ntile - 1) * kSub;
     const int nt = static_cast<int>(t1 - ts);
     load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
-    load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
-    load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
+    load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, ts, nt, gm.L, tid);
+    load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
+    if (gate) {
+      load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
+      load_xtile(pyr, bf.y_raw, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
+    }
     pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
     pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
     pck0 = load_ckpt(ts);
     pck1 = load_ckpt(ts + kCk);
+    stage_delta(pd);
+    stage_gate(pg, ts, nt);
     store_xtile(sU[0], pu, tid);
     store_xtile(sD[0], pd, tid);
     store_xtile(sG[0], pg, tid);
@@ -342,8 +420,12 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     if (more) {  // prefetch the previous tile (next in processing order)
       const int64_t tn = ts - kSub;
       load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pd, bf.delta, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pg, dy, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, tn, kSub, gm.L, tid);
+      load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
+      if (gate) {
+        load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, tn, kSub, gm.L, tid);
+        load_xtile(pyr, bf.y_raw, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
+      }
       pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
       pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
       pck0 = load_ckpt(tn);
@@ -365,6 +447,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     dDacc += static_cast<double>(tD);
     if (more) {
       __syncthreads();  // all flushes of the other buffer are done before it is refilled
+      stage_delta(pd);
+      stage_gate(pg, ts - kSub, kSub);
       store_xtile(sU[buf ^ 1], pu, tid);
       store_xtile(sD[buf ^ 1], pd, tid);
       store_xtile(sG[buf ^ 1], pg, tid);
@@ -380,6 +464,13 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) pa[jj] = dacc[jj];
     if (grp == 0) bf.part_dD[slot] = dDacc;
+  }
+  if (FUSE && bf.ddbias != nullptr) {  // dt_bias gradient: the 4 waves' rows, fixed order
+    sDb[wave][lane] = dbacc;
+    __syncthreads();
+    if (wave == 0 && dld < gm.D)
+      bf.part_db[(bk * gm.nchunk + chunk) * gm.D + dld] = (sDb[0][lane] + sDb[1][lane]) +
+                                                          (sDb[2][lane] + sDb[3][lane]);
   }
 }
 
@@ -421,36 +512,40 @@ reduce_ad_kernel(Geom gm, BwdBufs bf) {
       for (int64_t c = 0; c < gm.nchunk; ++c)
         s += bf.part_dA[(((b * gm.K + k) * gm.nchunk + c) * gm.D + d) * kStatePad + n];
     bf.dA[(k * gm.D + d) * gm.N + n] = static_cast<float>(s);
-  } else if (idx < nA + gm.K * gm.D) {
-    const int64_t i = idx - nA;
+  } else if (idx < nA + 2 * gm.K * gm.D) {
+    // dD, then (fused, when requested) the dt_bias gradient
+    const bool is_db = idx >= nA + gm.K * gm.D;
+    if (is_db && bf.ddbias == nullptr) return;
+    const int64_t i = idx - nA - (is_db ? gm.K * gm.D : 0);
     const int64_t d = i % gm.D;
     const int64_t k = i / gm.D;
+    const double* part = is_db ? bf.part_db : bf.part_dD;
     double s = 0.0;
     for (int64_t b = 0; b < gm.B; ++b)
       for (int64_t c = 0; c < gm.nchunk; ++c)
-        s += bf.part_dD[((b * gm.K + k) * gm.nchunk + c) * gm.D + d];
-    bf.dD[k * gm.D + d] = static_cast<float>(s);
+        s += part[((b * gm.K + k) * gm.nchunk + c) * gm.D + d];
+    (is_db ? bf.ddbias : bf.dD)[k * gm.D + d] = static_cast<float>(s);
   }
 }
 
-template <typename XT, typename OT>
+template <typename XT, typename OT, bool FUSE = false>
 static hipError_t launch_bwd_t(const Geom& g, const BwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   const int64_t tot_state = g.B * g.K * g.D * kStatePad;
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE>), grid_agg, block, 0, s, g, b);
     hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3(static_cast<unsigned>((tot_state + kThreads - 1) / kThreads)),
                        block, 0, s, g, b);
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_bwd_kernel<XT, OT>), grid, block, 0, s, g, b);
+  hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE>), grid, block, 0, s, g, b);
   const int64_t nbc = g.B * g.K * g.L * 2 * kStatePad;
   hipLaunchKernelGGL((reduce_bc_kernel<OT>), dim3(static_cast<unsigned>((nbc + kThreads - 1) / kThreads)),
                      block, 0, s, g, b);
-  const int64_t nad = g.K * g.D * (kStatePad + 1);
+  const int64_t nad = g.K * g.D * (kStatePad + 2);
   hipLaunchKernelGGL(reduce_ad_kernel, dim3(static_cast<unsigned>((nad + kThreads - 1) / kThreads)),
                      block, 0, s, g, b);
   return hipGetLastError();
@@ -461,6 +556,10 @@ hipError_t launch_bwd(const Geom& g, const BwdBufs& b, int in_dtype, int out_dty
   if (in_dtype == 1 && out_dtype == 1) return launch_bwd_t<bf16_t, bf16_t>(g, b, s);
   if (in_dtype == 1 && out_dtype == 0) return launch_bwd_t<bf16_t, float>(g, b, s);
   return launch_bwd_t<float, bf16_t>(g, b, s);
+}
+
+hipError_t launch_fused_bwd(const Geom& g, const BwdBufs& b, hipStream_t s) {
+  return launch_bwd_t<float, float, true>(g, b, s);
 }
 
 // --------------------------------------------------------------- utilities

@@ -66,6 +66,39 @@ __device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int6
   return r < 0 ? 0 : (r >= L ? L - 1 : r);
 }
 
+// Pointwise pieces of the fused block prologue / epilogue
+// (mamba_block.py:180-181, :190), on the transcendental unit (v_exp_f32,
+// v_log_f32, v_rcp_f32: a few ulp) rather than the libm routines, which
+// cost ~10x the instructions in VALU-bound kernels.
+//
+// log(1 + y) for y in (0, 1]: a 5-term series below 1/64 (truncation
+// < y^6 / 6 relative), else ln2 * log2(1 + y) (the rounding of 1 + y is
+// < 2^-24 absolute, < 2e-6 relative there).
+__device__ __forceinline__ float log1p_unit(float y) {
+  constexpr float kLn2 = 0.6931471805599453f;
+  if (y < 0.015625f)
+    return y * fmaf(y, fmaf(y, fmaf(y, fmaf(y, 0.2f, -0.25f), 1.f / 3.f), -0.5f), 1.f);
+  return kLn2 * __builtin_amdgcn_logf(1.f + y);
+}
+// softplus with torch.nn.functional's threshold (x > 20 -> x):
+// max(x, 0) + log(1 + e^-|x|)
+__device__ __forceinline__ float softplus_f(float x) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  const float r = fmaxf(x, 0.f) + log1p_unit(y);
+  return x > 20.f ? x : r;
+}
+// 1 / (1 + e^-x); saturates to 0 / 1 without NaN for large |x|
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+// d softplus(x) / dx = sigmoid(x) = 1 - e^-sp from the softplus value sp >= 0
+// (series below 1/64, where 1 - e^-sp would cancel)
+__device__ __forceinline__ float softplus_grad_from_value(float sp) {
+  if (sp < 0.015625f)
+    return sp * fmaf(sp, fmaf(sp, fmaf(sp, -1.f / 24.f, 1.f / 6.f), -0.5f), 1.f);
+  return 1.f - __builtin_amdgcn_exp2f(-sp * kLog2e);
+}
+
 // 2^x on the transcendental unit (v_exp_f32); callers pre-scale by log2(e).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -26,6 +26,13 @@
 //   pass 3 (kMain)   each chunk rescans from its carry-in, writes y and,
 //                    when training, the state after every 8th position
 //                    (the backward's checkpoints).
+//
+// Fused form (FUSE, float32): the block's prologue and epilogue around the
+// scan (mamba_block.py:180-181, :190) run inside the staging and write-back
+// of the same kernel: delta = softplus(delta_raw + dt_bias) as the delta tile
+// is staged, and y = y_raw * silu(z) as y is written back (y_raw kept for
+// the backward when requested), so neither delta nor the gate makes an
+// extra pass over HBM.
 #include "scan_common.h"
 #include "scan_kernels.h"
 
@@ -33,7 +40,7 @@ namespace mvm {
 
 enum FwdMode { kAgg = 0, kMain = 1 };
 
-template <typename XT, typename OT, int MODE>
+template <typename XT, typename OT, int MODE, bool FUSE>
 __global__ void __launch_bounds__(kThreads, 6)
 scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // double-buffered tile staging: u, delta (64 channels), B, C (16 states);
@@ -62,6 +69,9 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
   const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
   const int64_t xrow = b * gm.xsb + k * gm.xsk;            // + row * xst + channel
+  const int64_t drow = b * gm.dsb + k * gm.dsk;            // delta
+  const int64_t yrow = b * gm.ysb + k * gm.ysk;            // y, y_raw
+  const int64_t zrow = b * gm.zsb + k * gm.zsk;            // gate
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -70,6 +80,10 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
   OT* __restrict__ y = static_cast<OT*>(bf.y);
   float* __restrict__ ckpt = bf.ckpt;
+  // fused prologue: the dt bias of the channel this thread stages
+  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  const bool gate = FUSE && MODE == kMain && bf.z != nullptr;
+  float* __restrict__ y_raw = FUSE ? bf.y_raw : nullptr;
 
   float a2[4], h[4];
 #pragma unroll
@@ -90,16 +104,30 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // checkpoint slot s holds the state after position 8s + 7
   float* ckp = write_ck ? ckpt + (bk * gm.nck * gm.D + d) * kStatePad + 4 * grp : nullptr;
   const int64_t ck_stride = gm.D * kStatePad;
-  auto flush_y = [&](int buf, int64_t ts, int nt) {
+  // y of a staged tile (held in sU) back to HBM; zv = the gate values of the
+  // same rows and channel when fused
+  auto flush_y = [&](int buf, int64_t ts, int nt, const float (&zv)[4]) {
     const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lch = tid & 63;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
       if (tt < nt) {
-        OT* rowp = y + (xrow + token_row(tok, ts + tt, gm.L) * gm.xst + ch0);
-        if (dld < gm.D) st(rowp, lch, sU[buf][tt][lch]);
+        const int64_t row = token_row(tok, ts + tt, gm.L);
+        float v = sU[buf][tt][lch];
+        if (dld < gm.D) {
+          if (FUSE && y_raw != nullptr) y_raw[yrow + row * gm.yst + dld] = v;
+          if (gate) v *= zv[r] * sigmoid_f(zv[r]);
+          st(y + (yrow + row * gm.yst + ch0), lch, v);
+        }
       }
+    }
+  };
+  // fused prologue on the staged delta values
+  auto stage_delta = [&](float (&v)[4]) {
+    if (FUSE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = softplus_f(v[r] + dbias_l);
     }
   };
   // one scan step at tile position tt of buffer buf
@@ -132,13 +160,14 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   };
 
   const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
-  float pu[4], pd[4], pb = 0.f, pc = 0.f;
+  float pu[4], pd[4], pz[4] = {0.f, 0.f, 0.f, 0.f}, pb = 0.f, pc = 0.f;
   {
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - t0));
     load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, t0, nt, gm.L, tid);
-    load_xtile(pd, delta, xrow, dld, gm.D, gm.xst, tok, t0, nt, gm.L, tid);
+    load_xtile(pd, delta, drow, dld, gm.D, gm.dst, tok, t0, nt, gm.L, tid);
     pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
     if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
+    stage_delta(pd);
     store_xtile(sU[0], pu, tid);
     store_xtile(sD[0], pd, tid);
     sB[0][tid >> 4][tid & 15] = pb;
@@ -150,13 +179,15 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     const int64_t ts = t0 + it * kSub;
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
     __syncthreads();  // tile `it` staged; readers of the other buffer are done
-    if (write_y && it > 0) flush_y(buf ^ 1, ts - kSub, kSub);
+    if (write_y && it > 0) flush_y(buf ^ 1, ts - kSub, kSub, pz);
+    // gate values of this tile, used when it is flushed one tile later
+    if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
     const bool more = it + 1 < ntile;
     if (more) {  // prefetch the next tile; its latency overlaps this tile's math
       const int64_t tn = ts + kSub;
       const int ntn = static_cast<int>(min<int64_t>(kSub, t1 - tn));
       load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, ntn, gm.L, tid);
-      load_xtile(pd, delta, xrow, dld, gm.D, gm.xst, tok, tn, ntn, gm.L, tid);
+      load_xtile(pd, delta, drow, dld, gm.D, gm.dst, tok, tn, ntn, gm.L, tid);
       pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
       if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
     }
@@ -173,6 +204,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       }
     }
     if (more) {
+      stage_delta(pd);
       store_xtile(sU[buf ^ 1], pu, tid);
       store_xtile(sD[buf ^ 1], pd, tid);
       sB[buf ^ 1][tid >> 4][tid & 15] = pb;
@@ -182,7 +214,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   if (write_y) {
     __syncthreads();
     const int64_t ts = t0 + (ntile - 1) * kSub;
-    flush_y(static_cast<int>((ntile - 1) & 1), ts, static_cast<int>(t1 - ts));
+    flush_y(static_cast<int>((ntile - 1) & 1), ts, static_cast<int>(t1 - ts), pz);
   }
 
   if (MODE == kAgg && dvalid) {
@@ -217,20 +249,20 @@ scan_fwd_carry_kernel(Geom gm, FwdBufs bf) {
   }
 }
 
-template <typename XT, typename OT>
+template <typename XT, typename OT, bool FUSE = false>
 static hipError_t launch_fwd_t(const Geom& g, const FwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE>), grid_agg, block, 0, s, g, b);
     const int64_t total = g.B * g.K * g.D * kStatePad;
     hipLaunchKernelGGL(scan_fwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
                        block, 0, s, g, b);
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain>), grid, block, 0, s, g, b);
+  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain, FUSE>), grid, block, 0, s, g, b);
   return hipGetLastError();
 }
 
@@ -239,6 +271,10 @@ hipError_t launch_fwd(const Geom& g, const FwdBufs& b, int in_dtype, int out_dty
   if (in_dtype == 1 && out_dtype == 1) return launch_fwd_t<bf16_t, bf16_t>(g, b, s);
   if (in_dtype == 1 && out_dtype == 0) return launch_fwd_t<bf16_t, float>(g, b, s);
   return launch_fwd_t<float, bf16_t>(g, b, s);
+}
+
+hipError_t launch_fused_fwd(const Geom& g, const FwdBufs& b, hipStream_t s) {
+  return launch_fwd_t<float, float, true>(g, b, s);
 }
 
 }  // namespace mvm

@@ -10,7 +10,10 @@ namespace mvm {
 // Geometry of one scan call (all directions of one launch).
 struct Geom {
   int64_t B, L, D, N, K;
-  int64_t xsb, xsk, xst;   // u-like strides
+  int64_t xsb, xsk, xst;   // u, du strides
+  int64_t dsb, dsk, dst;   // delta, ddelta strides
+  int64_t ysb, ysk, yst;   // y, dy (and the fused y_raw) strides
+  int64_t zsb, zsk, zst;   // gate z, dz strides (fused form only)
   int64_t bsb, bsk, bst;   // B-like strides
   const int32_t* tok;      // (K, L) scan position -> token row, or nullptr
   int64_t chunk_len;       // multiple of kSub
@@ -30,6 +33,10 @@ struct FwdBufs {
   float* ckpt;     // may be null
   float* agg_h;    // (B*K, nchunk, D, 16): chunk end states, then carry-ins
   float* agg_s;    // (B*K, nchunk, D): sum of delta over each chunk
+  // fused form: delta = softplus(delta_raw + dbias), y = y_raw * silu(z)
+  const float* dbias;  // (K, D) or null (zero bias)
+  const float* z;      // gate or null (no gate)
+  float* y_raw;        // ungated output or null
 };
 
 struct BwdBufs {
@@ -52,6 +59,14 @@ struct BwdBufs {
   double* part_dA;  // (B*K, nchunk, D, 16) float64 partial sums
   double* part_dD;  // (B*K, nchunk, D)
   float* part_bc;  // (B*K, ncblk, L, 32): per channel-block dB | dC sums
+  // fused form: delta_raw / ddelta_raw in place of delta / ddelta
+  const float* dbias;  // (K, D) or null
+  float* ddbias;       // (K, D) gradient of dbias (when dbias is given)
+  double* part_db;     // (B*K, nchunk, D) float64 partials of ddbias
+  // fused gate y = y_raw * silu(z): dy is the gradient of the gated y
+  const float* z;      // z strides, or null (no gate)
+  const float* y_raw;  // y strides
+  float* dz;           // z strides
 };
 
 // in_dtype / out_dtype follow MVM_F32 / MVM_BF16.
@@ -59,6 +74,9 @@ hipError_t launch_fwd(const Geom& g, const FwdBufs& b, int in_dtype, int out_dty
                       hipStream_t s);
 hipError_t launch_bwd(const Geom& g, const BwdBufs& b, int in_dtype, int out_dtype,
                       hipStream_t s);
+// fused form (float32 only): softplus(delta_raw + dbias) on load, gate on store
+hipError_t launch_fused_fwd(const Geom& g, const FwdBufs& b, hipStream_t s);
+hipError_t launch_fused_bwd(const Geom& g, const BwdBufs& b, hipStream_t s);
 hipError_t launch_fill(float* p, int64_t n, float v, hipStream_t s);
 hipError_t launch_selftest_lanes(float* out, hipStream_t s);
 

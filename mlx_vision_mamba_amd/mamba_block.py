@@ -14,6 +14,15 @@ selective scan that read and write through per-direction index tables, the
 per-token projections batched over K, and one out_proj GEMM over the
 concatenated K*D_inner features, which is also the (atomic-free) sum over
 directions (:562-566).
+
+Between the two GEMMs the block core (conv + SiLU, x_proj, dt_proj, and the
+scan with the softplus of delta and the y * silu(z) gate fused into it,
+:170-190) is one autograd Function whose backward writes the gradient of
+the in_proj output in place: the conv's dx and the gate's dz land in the two
+halves of one buffer, so no slice / cat / elementwise pass is materialised.
+Activations between the projections are kept direction-major,
+(K, B*N, features), so the x_proj / dt_proj GEMMs batch over K without
+copies.
 """
 
 from __future__ import annotations
@@ -26,8 +35,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import directions as _dirs
-from .conv import causal_conv_silu
-from .scan import get_scan_fn, mode_chunk_len, selective_scan_directions
+from .conv import conv_silu_backward_into, conv_silu_forward_into
+from .scan import get_scan_fn, mode_chunk_len, scan_fused_backward, scan_fused_forward
 
 
 def _dt_bias_init(d_inner: int, dt_min: float = 1e-3, dt_max: float = 1e-1) -> torch.Tensor:
@@ -152,6 +161,80 @@ def _cached_table(cache, K, n, grid, device):
     return cache[key]
 
 
+def _bnkd(t_kbnd, bsz, n):
+    """(B, N, K, X) view of a direction-major (K, B*N, X) tensor."""
+    K, _, X = t_kbnd.shape
+    return t_kbnd.view(K, bsz, n, X).permute(1, 2, 0, 3)
+
+
+class _MambaCoreFn(torch.autograd.Function):
+    """xz (B, N, K, 2*D_inner) from in_proj -> gated scan output (B, N, K, D_inner).
+
+    Forward (mamba_block.py:166-190, all K directions at once):
+      xc    = silu(causal depthwise conv(x) + conv_b)      along each scan order
+      dbc   = x_proj(xc)                                   (K, B*N, R + 2N)
+      delta = softplus(dt_proj(dbc[:R]) + dt_bias)         inside the scan
+      y     = scan(xc, delta, -exp(A_log), B, C, D) * silu(z)
+    """
+
+    @staticmethod
+    def forward(ctx, xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, tok, chunk_len, detach):
+        bsz, n, K, d2 = xz.shape
+        din = d2 // 2
+        R = W_dt.shape[2]
+        ns = A_log.shape[2]
+        dev = xz.device
+        xb, z = xz[..., :din], xz[..., din:]
+        xc = torch.empty(K, bsz * n, din, dtype=torch.float32, device=dev)
+        conv_silu_forward_into(xb, conv_w, conv_b, _bnkd(xc, bsz, n), tok)       # :170-171
+        dbc = torch.bmm(xc, W_x.transpose(1, 2).contiguous())                      # :174
+        dt = dbc[..., :R]
+        delta_raw = torch.bmm(dt, W_dt.transpose(1, 2).contiguous())               # :180
+        A = -torch.exp(A_log)                                                      # :184
+        bc = _bnkd(dbc, bsz, n)
+        save = not detach
+        y, y_raw, ckpt = scan_fused_forward(_bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A,
+                                            bc[..., R:R + ns], bc[..., R + ns:], Dv, z, tok,
+                                            chunk_len, save=save)                  # :181, :187, :190
+        if save:
+            ctx.save_for_backward(xz, conv_w, conv_b, W_x, W_dt, b_dt, A, Dv, tok, xc, dbc,
+                                  delta_raw, y_raw, ckpt)
+            ctx.chunk_len = chunk_len
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (xz, conv_w, conv_b, W_x, W_dt, b_dt, A, Dv, tok, xc, dbc, delta_raw, y_raw,
+         ckpt) = ctx.saved_tensors
+        bsz, n, K, d2 = xz.shape
+        din = d2 // 2
+        R = W_dt.shape[2]
+        ns = A.shape[2]
+        dev = xz.device
+        xb, z = xz[..., :din], xz[..., din:]
+        dxz = torch.empty(xz.shape, dtype=torch.float32, device=dev)
+        d_dbc = torch.empty_like(dbc)
+        du = torch.empty_like(xc)
+        ddelta_raw = torch.empty_like(delta_raw)
+        bc, dbc_v = _bnkd(dbc, bsz, n), _bnkd(d_dbc, bsz, n)
+        _, _, db_dt, dA, _, _, dDv, _ = scan_fused_backward(
+            _bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A, bc[..., R:R + ns],
+            bc[..., R + ns:], Dv, z, y_raw, ckpt, dy, tok, ctx.chunk_len,
+            du=_bnkd(du, bsz, n), ddelta_raw=_bnkd(ddelta_raw, bsz, n),
+            dB=dbc_v[..., R:R + ns], dC=dbc_v[..., R + ns:], dz=dxz[..., din:])
+        # dt_proj: delta_raw = dt @ W_dt^T
+        d_dbc[..., :R] = torch.bmm(ddelta_raw, W_dt)
+        dW_dt = torch.bmm(ddelta_raw.transpose(1, 2), dbc[..., :R])
+        # x_proj: dbc = xc @ W_x^T; the scan's du joins through the GEMM's beta
+        dxc = torch.baddbmm(du, d_dbc, W_x)
+        dW_x = torch.bmm(d_dbc.transpose(1, 2), xc)
+        # conv + SiLU: dx lands in the first half of dxz
+        dconv_w, dconv_b = conv_silu_backward_into(xb, conv_w, conv_b, _bnkd(dxc, bsz, n),
+                                                   dxz[..., :din], tok)
+        dA_log = dA * A  # A = -exp(A_log)
+        return dxz, dconv_w, dconv_b, dW_x, dW_dt, db_dt, dA_log, dDv, None, None, None
+
+
 def _directional_forward(blocks, h, tok, scan_mode):
     """Run len(blocks) MambaBlocks on one (B, N, E) input, block k scanning
     in the order of tok[k], and return the sum of their outputs."""
@@ -160,29 +243,21 @@ def _directional_forward(blocks, h, tok, scan_mode):
     bsz, n, _ = h.shape
     din, ns, R = b0.d_inner, b0.d_state, b0.dt_rank
     W_in = torch.cat([blk.in_proj.weight for blk in blocks], 0) if K > 1 else b0.in_proj.weight
-    xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165
-    xb, z = xz[..., :din], xz[..., din:]                                       # :166-167
+    xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165-167
     conv_w = torch.cat([blk.conv1d.weight for blk in blocks], 0).view(K, din, b0.d_conv)
     conv_b = torch.cat([blk.conv1d.bias for blk in blocks], 0).view(K, din)
-    xc = causal_conv_silu(xb, conv_w, conv_b, tok)                             # :170-171
     W_x = torch.stack([blk.x_proj.weight for blk in blocks], 0)                # (K, R+2N, Din)
-    dbc = torch.matmul(xc.permute(2, 0, 1, 3).reshape(K, bsz * n, din),
-                       W_x.transpose(1, 2).contiguous())                       # :174
-    dbc = dbc.reshape(K, bsz, n, R + 2 * ns).permute(1, 2, 0, 3).contiguous()  # (B, N, K, R+2N)
-    dt = dbc[..., :R]                                                          # :175
-    Bm = dbc[..., R:R + ns]                                                    # :176
-    Cm = dbc[..., R + ns:]                                                     # :177
     W_dt = torch.stack([blk.dt_proj.weight for blk in blocks], 0)              # (K, Din, R)
     b_dt = torch.stack([blk.dt_proj.bias for blk in blocks], 0)                # (K, Din)
-    delta = torch.matmul(dt.permute(2, 0, 1, 3).reshape(K, bsz * n, R),
-                         W_dt.transpose(1, 2).contiguous())                    # :180
-    delta = delta.reshape(K, bsz, n, din).permute(1, 2, 0, 3) + b_dt
-    delta = F.softplus(delta).contiguous()                                     # :181
-    A = -torch.exp(torch.stack([blk.A_log for blk in blocks], 0))              # :184
+    A_log = torch.stack([blk.A_log for blk in blocks], 0)                      # (K, Din, N)
     Dv = torch.stack([blk.D for blk in blocks], 0)
-    y = selective_scan_directions(xc.contiguous(), delta, A, Bm, Cm, Dv, tok,
-                                  chunk_len=mode_chunk_len(scan_mode),
-                                  forward_only=(scan_mode == "metal"))         # :187
-    y = y * F.silu(z)                                                          # :190
+    if tok is not None:
+        tok = tok.to(h.device).contiguous()
+    # the reference's "metal" mode is inference only (mamba_metal.py:230)
+    detach = scan_mode == "metal"
+    args = [t.float() for t in (xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv)]
+    if detach:
+        args = [t.detach() for t in args]
+    y = _MambaCoreFn.apply(*args, tok, mode_chunk_len(scan_mode), detach)     # :170-190
     W_out = torch.cat([blk.out_proj.weight for blk in blocks], 1) if K > 1 else b0.out_proj.weight
     return F.linear(y.reshape(bsz, n, K * din), W_out)                         # :191, :562-566

@@ -58,6 +58,21 @@ def algorithmic_bytes(bsz, L, D, N, in_size, out_size, ndir=1):
     return fwd, vjp
 
 
+def algorithmic_bytes_fused(bsz, L, D, N, ndir=1, gate=True, bias=True):
+    """(forward, vjp) bytes of the fused form (float32): the plain scan's
+    tensors (delta_raw / ddelta_raw in place of delta / ddelta) plus, with a
+    gate, z and y_raw (written by the forward; read by the VJP, which also
+    writes dz), plus the dt bias and its gradient."""
+    fwd, vjp = algorithmic_bytes(bsz, L, D, N, 4, 4, ndir)
+    if gate:
+        fwd += bsz * L * D * (4 + 4)
+        vjp += bsz * L * D * (4 + 4 + 4)
+    if bias:
+        fwd += ndir * D * 4
+        vjp += ndir * D * 8
+    return fwd, vjp
+
+
 def _record(kind, u, Bm, in_dt, out_dt):
     bsz, L, K, D = u.shape
     fwd, vjp = algorithmic_bytes(bsz * K, L, D, Bm.shape[-1], _SIZE[in_dt], _SIZE[out_dt], K)
@@ -199,6 +214,160 @@ def scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt=None, tok=None, chunk_len=0,
             ev1.record()
             _timing.append(("bwd", ev0, ev1, _record("bwd", u, Bm, in_dt, out_dt)))
     return du, ddelta, dA, dB, dC, dD
+
+
+# ------------------------------------------------------------- fused form
+
+def _bkd(t):
+    """(b, t, k) strides of a (B, L, K, X) view."""
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _dense(t):
+    """True when t's strides are a permutation of a contiguous layout (no
+    gaps, no overlap), so empty_strided(t.shape, t.stride()) is compact."""
+    expected = 1
+    for st, sz in sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz != 1):
+        if st != expected:
+            return False
+        expected *= sz
+    return True
+
+
+def _fused_desc(u, delta_raw, Bm, y, z, tok, chunk_len):
+    fd = _lib.FusedDesc()
+    fd.scan = _make_desc(u, Bm, torch.float32, torch.float32, tok, chunk_len)
+    fd.dt_stride_b, fd.dt_stride_t, fd.dt_stride_k = _bkd(delta_raw)
+    fd.y_stride_b, fd.y_stride_t, fd.y_stride_k = _bkd(y)
+    if z is not None:
+        fd.z_stride_b, fd.z_stride_t, fd.z_stride_k = _bkd(z)
+    return fd
+
+
+def _check_fused(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z):
+    bsz, L, K, D = u.shape
+    N = A.shape[-1]
+    if delta_raw.shape != u.shape or (z is not None and z.shape != u.shape):
+        raise ValueError("u, delta_raw and z must share the (B, L, K, D) shape")
+    if A.shape != (K, D, N) or Bm.shape != (bsz, L, K, N) or Cm.shape != Bm.shape:
+        raise ValueError("A must be (K, D, N) and B, C (B, L, K, N)")
+    if Dv.shape != (K, D) or (delta_bias is not None and delta_bias.shape != (K, D)):
+        raise ValueError("D and the dt bias must be (K, D)")
+    if Bm.stride() != Cm.stride():
+        raise ValueError("B and C must share strides")
+    ts = [u, delta_raw, A, Bm, Cm, Dv] + [t for t in (delta_bias, z) if t is not None]
+    _check_device(*ts)
+    for t in ts:
+        if t.dtype != torch.float32 or t.stride(-1) != 1:
+            raise ValueError("the fused scan takes float32 views with channel stride 1")
+    if not (A.is_contiguous() and Dv.is_contiguous()
+            and (delta_bias is None or delta_bias.is_contiguous())):
+        raise ValueError("A, D and the dt bias must be contiguous")
+
+
+def scan_fused_forward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, tok=None, chunk_len=0,
+                       save=False):
+    """y = scan(u, softplus(delta_raw + delta_bias), A, B, C, D) * silu(z)
+    (mamba_block.py:180-190) in one launch sequence.
+
+    u, delta_raw, z: (B, L, K, D) float32 views with channel stride 1 and any
+    other strides (z may be None: no gate); delta_bias (K, D) or None;
+    A (K, D, N); Bm, Cm (B, L, K, N) views; Dv (K, D).  Returns
+    (y, y_raw, ckpt): y (B, L, K, D) contiguous; y_raw and ckpt are saved for
+    the backward when ``save`` (else None).
+    """
+    _check_fused(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z)
+    dev = u.device
+    L = u.shape[1]
+    y = torch.empty(u.shape, dtype=torch.float32, device=dev)
+    fd = _fused_desc(u, delta_raw, Bm, y, z, tok, _resolve_chunk(L, chunk_len))
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        y_raw = torch.empty_like(y) if (save and z is not None) else None
+        ckpt = None
+        if save:
+            ckpt = torch.empty(_lib.check(lib.mvm_scan_ckpt_elems(ctypes.byref(fd.scan))),
+                               dtype=torch.float32, device=dev)
+        nbytes = _lib.check(lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 0, int(z is not None)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        if _timing is not None:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        _lib.check(lib.mvm_scan_fused_fwd(
+            ctypes.byref(fd), _ptr(u), _ptr(delta_raw), _ptr(delta_bias), _ptr(A), _ptr(Bm),
+            _ptr(Cm), _ptr(Dv), _ptr(z), _ptr(y), _ptr(y_raw), _ptr(ckpt), _ptr(ws), nbytes,
+            ctypes.c_void_p(_stream_ptr(dev))))
+        if _timing is not None:
+            ev1.record()
+            bsz, _, K, D = u.shape
+            nb = algorithmic_bytes_fused(bsz * K, L, D, A.shape[-1], K, z is not None,
+                                         delta_bias is not None)[0]
+            _timing.append(("fwd", ev0, ev1, nb))
+    return y, y_raw, ckpt
+
+
+def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt, dy, tok=None,
+                        chunk_len=0, du=None, ddelta_raw=None, dB=None, dC=None, dz=None):
+    """VJP of scan_fused_forward for dy (gradient of the gated y).
+
+    Output views may be passed in (any strides with channel stride 1, e.g.
+    slices of a larger gradient buffer); missing ones are allocated with
+    the layout of their primal.  Returns (du, ddelta_raw, ddelta_bias, dA,
+    dB, dC, dD, dz); ddelta_bias is None without a bias, dz None without a
+    gate.
+    """
+    _check_fused(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z)
+    dev = u.device
+    L = u.shape[1]
+    if dy.shape != u.shape:
+        raise ValueError(f"dy shape {tuple(dy.shape)} != {tuple(u.shape)}")
+    # dy and y_raw share the y strides of the descriptor
+    ref = y_raw if (z is not None and y_raw is not None) else None
+    if ref is not None and not ref.is_contiguous():
+        raise ValueError("y_raw must be contiguous")
+    if dy.dtype != torch.float32 or not dy.is_contiguous():
+        dy = dy.float().contiguous()
+
+    def like(t):
+        if not _dense(t):
+            raise ValueError("pass an output view for a primal with gaps in its layout")
+        return torch.empty_strided(t.shape, t.stride(), dtype=torch.float32, device=dev)
+
+    du = like(u) if du is None else du
+    ddelta_raw = like(delta_raw) if ddelta_raw is None else ddelta_raw
+    if dB is None or dC is None:
+        dB = torch.empty_strided(Bm.shape, Bm.stride(), dtype=torch.float32, device=dev)
+        dC = torch.empty_strided(Bm.shape, Bm.stride(), dtype=torch.float32, device=dev)
+    if dB.stride() != Bm.stride() or dC.stride() != Bm.stride():
+        raise ValueError("dB and dC must have the strides of B")
+    if z is not None and dz is None:
+        dz = like(z)
+    if (z is not None and dz.stride() != z.stride()) or ddelta_raw.stride() != delta_raw.stride() \
+            or du.stride() != u.stride():
+        raise ValueError("gradient views must have the strides of their primals")
+    ddelta_bias = torch.empty_like(delta_bias) if delta_bias is not None else None
+    dA = torch.empty(A.shape, dtype=torch.float32, device=dev)
+    dD = torch.empty(Dv.shape, dtype=torch.float32, device=dev)
+    fd = _fused_desc(u, delta_raw, Bm, dy, z, tok, _resolve_chunk(L, chunk_len))
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        nbytes = _lib.check(lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, int(z is not None)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        if _timing is not None:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        _lib.check(lib.mvm_scan_fused_bwd(
+            ctypes.byref(fd), _ptr(u), _ptr(delta_raw), _ptr(delta_bias), _ptr(A), _ptr(Bm),
+            _ptr(Cm), _ptr(Dv), _ptr(z), _ptr(y_raw), _ptr(ckpt), _ptr(dy), _ptr(du),
+            _ptr(ddelta_raw), _ptr(ddelta_bias), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz),
+            _ptr(ws), nbytes, ctypes.c_void_p(_stream_ptr(dev))))
+        if _timing is not None:
+            ev1.record()
+            bsz, _, K, D = u.shape
+            nb = algorithmic_bytes_fused(bsz * K, L, D, A.shape[-1], K, z is not None,
+                                         delta_bias is not None)[1]
+            _timing.append(("bwd", ev0, ev1, nb))
+    return du, ddelta_raw, ddelta_bias, dA, dB, dC, dD, dz
 
 
 class _SelectiveScanFn(torch.autograd.Function):

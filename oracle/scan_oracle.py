@@ -17,6 +17,10 @@ Pinning (each function is checked by something other than a retyped formula):
                       closed forms dD = sum(g*u) and the delta=0 dδ formula.
 * ``scan_fwd_chunked`` equals ``scan_fwd`` for chunk=1, chunk=L and any chunk.
 * ``combine``          associativity, checked numerically.
+* ``fused_fwd`` / ``fused_vjp``  (the block's softplus prologue and gated
+                      epilogue around the scan) torch float64 autograd through
+                      ``F.softplus`` / ``F.silu`` and the independent torch
+                      scan restatement; tests/test_oracle.py.
 
 No golden vectors exist in the reference (it has no tests); the fixtures under
 tests/golden/ are written by this oracle after the checks above pass.
@@ -167,6 +171,63 @@ def scan_vjp(u, delta, A, B, C, D, g):
         lam = lam * e                                                 # :136
     dD = np.sum(g * u, axis=(0, 1))                                   # :89, :214
     return du, ddelta, dA, dB, dC, dD
+
+
+# ---------------------------------------------------------------------------
+# Block prologue / epilogue around the scan (the fused form)
+# ---------------------------------------------------------------------------
+
+def softplus(x):
+    """softplus as the block applies it to dt_proj's output
+    (mamba_block.py:181), with torch's linear branch above x = 20."""
+    x = np.asarray(x, dtype=np.float64)
+    return np.where(x > 20.0, x, np.logaddexp(0.0, x))
+
+
+def sigmoid(x):
+    """1 / (1 + e^-x), evaluated without overflow for either sign of x."""
+    x = np.asarray(x, dtype=np.float64)
+    e = np.exp(-np.abs(x))
+    return np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def fused_fwd(u, delta_raw, bias, A, B, C, D, z):
+    """mamba_block.py:180-190 around the scan:
+        delta = softplus(delta_raw + bias)   (:180-181, bias = dt_proj.bias)
+        y_raw = scan(u, delta, A, B, C, D)   (:187)
+        y     = y_raw * silu(z)              (:190)
+    bias may be None (zero), z None (no gate).  Returns (y, y_raw, delta)."""
+    delta_raw = np.asarray(delta_raw, dtype=np.float64)
+    x = delta_raw + (0.0 if bias is None else np.asarray(bias, dtype=np.float64))
+    delta = softplus(x)
+    y_raw = scan_fwd(u, delta, A, B, C, D)
+    if z is None:
+        return y_raw, y_raw, delta
+    z = np.asarray(z, dtype=np.float64)
+    return y_raw * z * sigmoid(z), y_raw, delta
+
+
+def fused_vjp(u, delta_raw, bias, A, B, C, D, z, g):
+    """VJP of ``fused_fwd`` for upstream g (the gradient of the gated y):
+    the gate's product and silu derivatives, ``scan_vjp`` on
+    g * silu(z), and softplus' derivative (sigmoid; 1 above the threshold).
+    Returns (du, ddelta_raw, dbias, dA, dB, dC, dD, dz); dbias sums over
+    (b, t), dz is None without a gate."""
+    delta_raw, g = _f64(delta_raw, g)
+    x = delta_raw + (0.0 if bias is None else np.asarray(bias, dtype=np.float64))
+    delta = softplus(x)
+    if z is None:
+        gs, dz = g, None
+    else:
+        z = np.asarray(z, dtype=np.float64)
+        s = sigmoid(z)
+        y_raw = scan_fwd(u, delta, A, B, C, D)
+        gs = g * z * s
+        dz = g * y_raw * s * (1.0 + z * (1.0 - s))
+    du, dd, dA, dB, dC, dD = scan_vjp(u, delta, A, B, C, D, gs)
+    ddelta_raw = dd * np.where(x > 20.0, 1.0, sigmoid(x))
+    dbias = ddelta_raw.sum(axis=(0, 1))
+    return du, ddelta_raw, dbias, dA, dB, dC, dD, dz
 
 
 # ---------------------------------------------------------------------------

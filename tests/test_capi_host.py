@@ -160,6 +160,7 @@ def _cdesc(B=2, L=20, D=24, K=1, kc=4):
     d.batch, d.seqlen, d.dim, d.ndir, d.kwidth = B, L, D, K, kc
     d.x_stride_b, d.x_stride_t, d.x_stride_k = L * K * 2 * D, K * 2 * D, 2 * D
     d.y_stride_b, d.y_stride_t, d.y_stride_k = L * K * D, K * D, D
+    d.dx_stride_b, d.dx_stride_t, d.dx_stride_k = L * K * D, K * D, D
     return d
 
 
@@ -167,6 +168,7 @@ def _cdesc(B=2, L=20, D=24, K=1, kc=4):
     ("kwidth", 9, _lib.MVM_ERR_UNSUPPORTED), ("kwidth", 0, _lib.MVM_ERR_UNSUPPORTED),
     ("ndir", 0, _lib.MVM_ERR_INVALID_ARG), ("batch", -2, _lib.MVM_ERR_INVALID_ARG),
     ("y_stride_t", 3, _lib.MVM_ERR_INVALID_ARG), ("x_stride_k", -1, _lib.MVM_ERR_INVALID_ARG),
+    ("dx_stride_t", 3, _lib.MVM_ERR_INVALID_ARG), ("dx_stride_b", -1, _lib.MVM_ERR_INVALID_ARG),
 ])
 def test_conv_bad_descriptors_rejected(field, value, code):
     lib = _lib.lib()
@@ -186,3 +188,70 @@ def test_conv_null_and_workspace_rejected_before_launch():
     need = lib.mvm_conv_workspace_bytes(ctypes.byref(d))
     rc = lib.mvm_conv_silu_bwd(ctypes.byref(d), *([fake] * 8), need - 1, null)
     assert rc == _lib.MVM_ERR_WORKSPACE
+
+
+def _fdesc(B=2, L=40, D=24, N=16, K=3):
+    fd = _lib.FusedDesc()
+    fd.scan = _desc(B, L, D, N, K)
+    # delta_raw (K, B, L, D); y (B, L, K, D); z a strided half of (B, L, K, 2D)
+    fd.dt_stride_k, fd.dt_stride_b, fd.dt_stride_t = B * L * D, L * D, D
+    fd.y_stride_b, fd.y_stride_t, fd.y_stride_k = L * K * D, K * D, D
+    fd.z_stride_b, fd.z_stride_t, fd.z_stride_k = L * K * 2 * D, K * 2 * D, 2 * D
+    return fd
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dt_stride_t", 3, _lib.MVM_ERR_INVALID_ARG), ("y_stride_b", -1, _lib.MVM_ERR_INVALID_ARG),
+    ("z_stride_t", 5, _lib.MVM_ERR_INVALID_ARG),
+])
+def test_fused_bad_descriptors_rejected(field, value, code):
+    lib = _lib.lib()
+    fd = _fdesc()
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == 0
+    for which, gate in ((0, 0), (1, 0), (1, 1)):
+        assert lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), which, gate) >= 0
+    setattr(fd, field, value)
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == code
+
+
+def test_fused_is_float32_only():
+    lib = _lib.lib()
+    fd = _fdesc()
+    fd.scan.in_dtype = _lib.MVM_BF16
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == _lib.MVM_ERR_UNSUPPORTED
+    assert "float32" in _lib.last_error()
+
+
+def test_fused_gate_needs_no_extra_workspace():
+    """The gate's backward runs inside the scan's staging: no dense buffer."""
+    lib = _lib.lib()
+    fd = _fdesc()
+    plain = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 0)
+    gated = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1)
+    assert gated == plain > 0
+
+
+def test_fused_null_pointers_rejected_before_launch():
+    lib = _lib.lib()
+    fd = _fdesc()
+    null = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)
+    # forward without y
+    args = [fake] * 12
+    args[8] = null
+    assert lib.mvm_scan_fused_fwd(ctypes.byref(fd), *args, 0, null) == _lib.MVM_ERR_INVALID_ARG
+    # backward: a gate (z) without y_raw
+    bargs = [fake] * 20
+    bargs[8] = fake   # z
+    bargs[9] = null   # y_raw
+    need = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1)
+    rc = lib.mvm_scan_fused_bwd(ctypes.byref(fd), *bargs, need, null)
+    assert rc == _lib.MVM_ERR_INVALID_ARG
+    # backward: delta_bias without ddelta_bias
+    bargs = [fake] * 20
+    bargs[12] = null  # ddelta_bias
+    assert lib.mvm_scan_fused_bwd(ctypes.byref(fd), *bargs, need, null) == _lib.MVM_ERR_INVALID_ARG
+    # backward without checkpoints
+    bargs = [fake] * 20
+    bargs[9 + 1] = null  # ckpt
+    assert lib.mvm_scan_fused_bwd(ctypes.byref(fd), *bargs, need, null) == _lib.MVM_ERR_INVALID_ARG

@@ -147,6 +147,53 @@ def test_torch_restatement_gradcheck():
                                     eps=1e-6, atol=1e-7)
 
 
+# ------------------------------------------------- fused prologue / epilogue
+
+def _fused_case(bsz, L, D, N, seed, gate=True, bias=True):
+    *args, g = _rand(bsz, L, D, N, seed=seed, a_mode="random")
+    rng = np.random.default_rng(seed)
+    u, _, A, Bm, Cm, Dv = args
+    # pre-activations that reach both softplus branches (x > 20 included)
+    draw = rng.standard_normal((bsz, L, D)) * 3.0 - 2.0
+    draw[0, 0, 0] = 25.0
+    b = rng.standard_normal(D) * 0.5 if bias else None
+    z = rng.standard_normal((bsz, L, D)) * 2.0 if gate else None
+    return u, draw, b, A, Bm, Cm, Dv, z, g
+
+
+@pytest.mark.parametrize("gate,bias", [(True, True), (False, True), (True, False)])
+def test_fused_matches_torch_autograd(gate, bias):
+    """The block's softplus prologue and silu gate around the scan, against
+    torch float64 autograd through F.softplus / F.silu and the independent
+    torch scan restatement."""
+    u, draw, b, A, Bm, Cm, Dv, z, g = _fused_case(2, 11, 5, 6, seed=21, gate=gate, bias=bias)
+    F = torch.nn.functional
+    t = {k: torch.tensor(v, dtype=torch.float64, requires_grad=True)
+         for k, v in dict(u=u, draw=draw, A=A, Bm=Bm, Cm=Cm, Dv=Dv).items()}
+    tb = torch.tensor(b, requires_grad=True) if bias else None
+    tz = torch.tensor(z, requires_grad=True) if gate else None
+    x = t["draw"] + tb if bias else t["draw"]
+    y_raw = torch_ref.scan_sequential(t["u"], F.softplus(x), t["A"], t["Bm"], t["Cm"], t["Dv"])
+    y = y_raw * F.silu(tz) if gate else y_raw
+    leaves = [t["u"], t["draw"]] + ([tb] if bias else []) + [t["A"], t["Bm"], t["Cm"], t["Dv"]] + \
+        ([tz] if gate else [])
+    ref = [r.numpy() for r in torch.autograd.grad(y, leaves, torch.tensor(g))]
+    y_o, y_raw_o, _ = so.fused_fwd(u, draw, b, A, Bm, Cm, Dv, z)
+    np.testing.assert_allclose(y_o, y.detach().numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(y_raw_o, y_raw.detach().numpy(), rtol=1e-12, atol=1e-13)
+    du, ddr, db, dA, dB, dC, dD, dz = so.fused_vjp(u, draw, b, A, Bm, Cm, Dv, z, g)
+    ours = [du, ddr] + ([db] if bias else []) + [dA, dB, dC, dD] + ([dz] if gate else [])
+    for i, (a, r) in enumerate(zip(ours, ref)):
+        np.testing.assert_allclose(a, r, rtol=1e-10, atol=1e-12, err_msg=f"grad {i}")
+
+
+def test_softplus_threshold_and_sigmoid():
+    x = np.array([-50.0, -1.0, 0.0, 3.0, 19.9, 20.0, 20.1, 60.0])
+    ref = torch.nn.functional.softplus(torch.tensor(x)).numpy()
+    np.testing.assert_allclose(so.softplus(x), ref, rtol=1e-15, atol=0)
+    np.testing.assert_allclose(so.sigmoid(x), torch.sigmoid(torch.tensor(x)).numpy(), rtol=1e-15)
+
+
 def test_vjp_closed_forms():
     *args, g = _rand(2, 11, 3, 4, seed=12)
     du, ddelta, dA, dB, dC, dD = so.scan_vjp(*args, g)
