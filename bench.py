@@ -13,7 +13,8 @@ loss + backward + AdamW update.  Inputs are resident on the GPU before the
 timed region; W untimed warm-up steps, then exactly K steps between two
 device synchronisations.  value = images / second.
 
-roofline: the selective-scan backward call (the largest hand-written piece
+roofline: the fused scan backward call (the block's scan VJP with the
+softplus and silu-gate gradients inside it; the largest hand-written piece
 of the step; its kernels are listed in "kernel"), timed with HIP events on
 the stream it runs on for every launch inside the timed region; achieved =
 algorithmic bytes per launch / mean launch time, against the MI355X HBM3E
@@ -45,7 +46,8 @@ if ROOT not in sys.path:
 
 METRIC = "selective-scan fwd+VJP GB/s & % HBM peak; VisionMamba-2D train imgs/sec"
 HBM_PEAK_GBS = 8000.0
-BWD_KERNELS = "mvm_scan_bwd: scan_bwd_agg_kernel + scan_bwd_carry_kernel + scan_bwd_kernel + reduce_bc_kernel + reduce_ad_kernel"
+BWD_KERNELS = ("mvm_scan_fused_bwd: scan_bwd_kernel<float, float, fused> + reduce_bc_kernel + "
+               "reduce_ad_kernel (one time chunk at this shape, so no agg / carry pass)")
 
 
 def _seeded_model(torch, mvm, device):
@@ -125,26 +127,35 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
 
 
 def step_scan_inputs(torch, device):
-    """The scan call of one VisionMamba-2D layer of the step: B=32, K=4
-    directions of a 14x14 grid (L=196), D=768, N=16, fp32, B and C as
-    strided column slices of a (B, L, K, 24 + 2N) projection output."""
+    """The fused scan call of one VisionMamba-2D layer of the step, in the
+    block's layouts: B=32, K=4 directions of a 14x14 grid (L=196), D=768,
+    N=16, dt_rank 24, fp32; u and delta_raw direction-major (K, B*L, D),
+    B and C column slices of the x_proj output (K, B*L, 24 + 2N), z the
+    second half of the in_proj output (B, L, K, 2D)."""
     from mlx_vision_mamba_amd import directions
-    bsz, L, K, D, N = 32, 196, 4, 768, 16
+    bsz, L, K, D, N, R = 32, 196, 4, 768, 16, 24
     g = torch.Generator().manual_seed(0)
-    u = torch.randn(bsz, L, K, D, generator=g).to(device)
-    dl = torch.nn.functional.softplus(torch.randn(bsz, L, K, D, generator=g) * 0.5 - 4.6).to(device)
+
+    def bnkd(t):
+        return t.view(K, bsz, L, t.shape[-1]).permute(1, 2, 0, 3)
+
+    u = torch.randn(K, bsz * L, D, generator=g).to(device)
+    draw = (torch.randn(K, bsz * L, D, generator=g) * 0.5 - 4.6).to(device)
+    bias = (torch.randn(K, D, generator=g) * 0.1).to(device)
     A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(K, D, 1).to(device)
-    dbc = torch.randn(bsz, L, K, 24 + 2 * N, generator=g).to(device)
-    Bm, Cm = dbc[..., 24:24 + N], dbc[..., 24 + N:]
+    dbc = torch.randn(K, bsz * L, R + 2 * N, generator=g).to(device)
+    bc = bnkd(dbc)
     Dv = torch.ones(K, D, device=device)
+    xz = torch.randn(bsz, L, K, 2 * D, generator=g).to(device)
     dy = torch.randn(bsz, L, K, D, generator=g).to(device)
     tok = directions.seq_to_tok_table(K, L, (14, 14)).to(device)
-    return (u, dl, A, Bm, Cm, Dv), dy, tok
+    args = (bnkd(u), bnkd(draw), bias, A, bc[..., R:R + N], bc[..., R + N:], Dv, xz[..., D:])
+    return args, dy, tok
 
 
 def scan_driver(torch, scan, device):
     """Profiling driver (--scan-driver): one 512 MiB device copy, whose HBM
-    traffic is known and calibrates the byte counters, then two scan
+    traffic is known and calibrates the byte counters, then two fused scan
     forward + VJP calls at the VisionMamba step shape."""
     src = torch.empty(128 * 1024 * 1024, dtype=torch.float32, device=device).uniform_()
     dst = torch.empty_like(src)
@@ -152,11 +163,18 @@ def scan_driver(torch, scan, device):
     torch.cuda.synchronize()
     del src, dst
     args, dy, tok = step_scan_inputs(torch, device)
+    dxz = torch.empty(args[7].shape[:3] + (2 * args[7].shape[3],), device=device)
+    d_dbc = torch.empty(args[4].shape[2], args[4].shape[0] * args[4].shape[1],
+                        args[4].stride(1), device=device)
+    R, N = 24, args[3].shape[-1]
+    dbc_v = d_dbc.view(d_dbc.shape[0], args[4].shape[0], args[4].shape[1], -1).permute(1, 2, 0, 3)
     for _ in range(2):
-        y, ck = scan.scan_forward(*args, tok, save_ckpt=True)
-        scan.scan_backward(*args, dy, ckpt=ck, tok=tok)
+        y, y_raw, ck = scan.scan_fused_forward(*args, tok=tok, save=True)
+        scan.scan_fused_backward(*args, y_raw, ck, dy, tok=tok, dB=dbc_v[..., R:R + N],
+                                 dC=dbc_v[..., R + N:], dz=dxz[..., args[7].shape[3]:])
     torch.cuda.synchronize()
-    print(json.dumps({"scan_driver": "done", "shape": "B=32 L=196 K=4 D=768 N=16 fp32"}), flush=True)
+    print(json.dumps({"scan_driver": "done", "shape": "B=32 L=196 K=4 D=768 N=16 fp32 fused"}),
+          flush=True)
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")

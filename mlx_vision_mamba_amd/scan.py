@@ -223,14 +223,14 @@ def _bkd(t):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
-def _dense(t):
-    """True when t's strides are a permutation of a contiguous layout (no
-    gaps, no overlap), so empty_strided(t.shape, t.stride()) is compact."""
-    expected = 1
+def _no_overlap(t):
+    """True when no two elements of t share memory: ordered by stride, each
+    dimension's stride clears the span of the smaller ones."""
+    span = 1
     for st, sz in sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz != 1):
-        if st != expected:
+        if st < span:
             return False
-        expected *= sz
+        span = st * sz
     return True
 
 
@@ -329,8 +329,9 @@ def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt,
         dy = dy.float().contiguous()
 
     def like(t):
-        if not _dense(t):
-            raise ValueError("pass an output view for a primal with gaps in its layout")
+        # same strides as the primal (a layout with gaps allocates its span)
+        if not _no_overlap(t):
+            raise ValueError("a primal whose elements overlap (e.g. broadcast) needs an output view")
         return torch.empty_strided(t.shape, t.stride(), dtype=torch.float32, device=dev)
 
     du = like(u) if du is None else du
