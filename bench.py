@@ -9,7 +9,7 @@ batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
 384 (d_inner 768), d_state 16, depth 6, float32 random-init weights
 (Kaiming-uniform projections, S4D-real A, dt bias with softplus(bias) in
 [1e-3, 1e-1]); loss = mean of the output features; one step = forward +
-loss + backward + AdamW update.  Inputs are resident on the GPU before the
+loss + backward + AdamW update (torch's fused AdamW).  Inputs are resident on the GPU before the
 timed region; W untimed warm-up steps, then exactly K steps between two
 device synchronisations.  value = images / second.
 
@@ -61,7 +61,7 @@ def bench_step(torch, mvm, scan, steps, warmup, device):
     model = _seeded_model(torch, mvm, device)
     gen = torch.Generator().manual_seed(1)
     x = torch.randn(32, 224, 224, 1, generator=gen).to(device)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
 
     def step():
         opt.zero_grad(set_to_none=True)

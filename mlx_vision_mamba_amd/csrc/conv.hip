@@ -22,7 +22,29 @@ namespace mvm {
 constexpr int kCvPos = 16;        // positions per wave
 constexpr int kCvBlockPos = 64;   // positions per block
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+// Token rows are looked up in uniform control flow (scalar loads through
+// the constant address space) and every row load goes to an in-bounds,
+// clamped address whose value is then selected away when the position or
+// channel is out of range: no load sits behind a divergent branch, so the
+// window's loads issue back to back instead of waiting one by one.
+template <bool TOK>
+__device__ __forceinline__ int64_t row_of(const int32_t* tok, int64_t p, int64_t L) {
+  if constexpr (TOK) {
+    const int64_t r = ((const const_i32*)tok)[p];
+    return r < 0 ? 0 : (r >= L ? L - 1 : r);
+  } else {
+    return p;
+  }
+}
+template <bool TOK>
+__device__ __forceinline__ int64_t safe_row(const int32_t* tok, int64_t p, int64_t L) {
+  return row_of<TOK>(tok, p < 0 ? 0 : (p >= L ? L - 1 : p), L);
+}
+// v, or +0 when the (wave-uniform) position is outside [0, L): a bit mask
+// rather than a select, so the load is not moved under a branch
+__device__ __forceinline__ float keep_if(float v, bool in_range) {
+  return __uint_as_float(__float_as_uint(v) & (in_range ? ~0u : 0u));
+}
 
 // one position's pre-activation from a window w[0..kc) over x[s-kc+1 .. s]
 template <int KC>
@@ -33,7 +55,7 @@ __device__ __forceinline__ float conv_at(const float* wv, const float* xw, float
   return acc;
 }
 
-template <int KC>
+template <int KC, bool TOK>
 __global__ void __launch_bounds__(kThreads)
 conv_fwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict__ w,
                 const float* __restrict__ bias, float* __restrict__ y) {
@@ -41,35 +63,38 @@ conv_fwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
   const int wave = threadIdx.x >> 6;
   const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + lane;
   const bool dvalid = d < g.D;
+  const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / g.K, k = bk - (bk / g.K) * g.K;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos + wave * kCvPos;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos +
+                     __builtin_amdgcn_readfirstlane(wave) * kCvPos;
   if (s0 >= g.L) return;
   const int32_t* tok = g.tok ? g.tok + k * g.L : nullptr;
-  const int64_t xb = b * g.xsb + k * g.xsk;
-  const int64_t yb = b * g.ysb + k * g.ysk;
+  const float* xb = x + b * g.xsb + k * g.xsk + dc;
+  float* yb = y + b * g.ysb + k * g.ysk + dc;
   float wv[KC];
 #pragma unroll
-  for (int j = 0; j < KC; ++j) wv[j] = dvalid ? w[(k * g.D + d) * KC + j] : 0.f;
-  const float bs = dvalid ? bias[k * g.D + d] : 0.f;
+  for (int j = 0; j < KC; ++j) wv[j] = w[(k * g.D + dc) * KC + j];
+  const float bs = bias[k * g.D + dc];
   // window: xw[i] = x at position s0 - (KC-1) + i
   float xw[kCvPos + KC - 1];
 #pragma unroll
+  for (int i = 0; i < kCvPos + KC - 1; ++i) xw[i] = xb[safe_row<TOK>(tok, s0 - (KC - 1) + i, g.L) * g.xst];
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
+#pragma unroll
   for (int i = 0; i < kCvPos + KC - 1; ++i) {
     const int64_t p = s0 - (KC - 1) + i;
-    xw[i] = (dvalid && p >= 0 && p < g.L) ? x[xb + token_row(tok, p, g.L) * g.xst + d] : 0.f;
+    xw[i] = keep_if(xw[i], p >= 0 && p < g.L);
   }
 #pragma unroll
   for (int i = 0; i < kCvPos; ++i) {
     const int64_t p = s0 + i;
-    if (p < g.L && dvalid) {
-      const float pre = conv_at<KC>(wv, xw + i, bs);
-      y[yb + token_row(tok, p, g.L) * g.yst + d] = pre * sigmoidf_(pre);
-    }
+    const float pre = conv_at<KC>(wv, xw + i, bs);
+    if (p < g.L && dvalid) yb[row_of<TOK>(tok, p, g.L) * g.yst] = pre * sigmoid_f(pre);
   }
 }
 
-template <int KC>
+template <int KC, bool TOK>
 __global__ void __launch_bounds__(kThreads)
 conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict__ w,
                 const float* __restrict__ bias, const float* __restrict__ dy,
@@ -79,38 +104,42 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
   const int wave = threadIdx.x >> 6;
   const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + lane;
   const bool dvalid = d < g.D;
+  const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / g.K, k = bk - (bk / g.K) * g.K;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos + wave * kCvPos;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos +
+                     __builtin_amdgcn_readfirstlane(wave) * kCvPos;
   const int32_t* tok = g.tok ? g.tok + k * g.L : nullptr;
-  const int64_t xb = b * g.xsb + k * g.xsk;
-  const int64_t yb = b * g.ysb + k * g.ysk;
-  const int64_t dxb = b * g.dxsb + k * g.dxsk;
+  const float* xb = x + b * g.xsb + k * g.xsk + dc;
+  const float* dyb = dy + b * g.ysb + k * g.ysk + dc;
+  float* dxb = dx + b * g.dxsb + k * g.dxsk + dc;
   float wv[KC];
 #pragma unroll
-  for (int j = 0; j < KC; ++j) wv[j] = dvalid ? w[(k * g.D + d) * KC + j] : 0.f;
-  const float bs = dvalid ? bias[k * g.D + d] : 0.f;
+  for (int j = 0; j < KC; ++j) wv[j] = w[(k * g.D + dc) * KC + j];
+  const float bs = bias[k * g.D + dc];
   // x at positions s0 - (KC-1) .. s0 + kCvPos - 1 + (KC-1)
   constexpr int kXW = kCvPos + 2 * (KC - 1);
   float xw[kXW];
 #pragma unroll
-  for (int i = 0; i < kXW; ++i) {
-    const int64_t p = s0 - (KC - 1) + i;
-    xw[i] = (dvalid && p >= 0 && p < g.L) ? x[xb + token_row(tok, p, g.L) * g.xst + d] : 0.f;
-  }
+  for (int i = 0; i < kXW; ++i) xw[i] = xb[safe_row<TOK>(tok, s0 - (KC - 1) + i, g.L) * g.xst];
   // dpre at positions s0 .. s0 + kCvPos - 1 + (KC-1)
   constexpr int kGW = kCvPos + KC - 1;
   float gp[kGW];
 #pragma unroll
+  for (int i = 0; i < kGW; ++i) gp[i] = dyb[safe_row<TOK>(tok, s0 + i, g.L) * g.yst];
+  __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
+#pragma unroll
+  for (int i = 0; i < kXW; ++i) {
+    const int64_t p = s0 - (KC - 1) + i;
+    xw[i] = keep_if(xw[i], p >= 0 && p < g.L);
+  }
+#pragma unroll
+  for (int i = 0; i < kGW; ++i) gp[i] = keep_if(gp[i], s0 + i < g.L);
+#pragma unroll
   for (int i = 0; i < kGW; ++i) {
-    const int64_t p = s0 + i;
-    float v = 0.f;
-    if (dvalid && p < g.L) {
-      const float pre = conv_at<KC>(wv, xw + i, bs);
-      const float sg = sigmoidf_(pre);
-      v = dy[yb + token_row(tok, p, g.L) * g.yst + d] * sg * (1.f + pre * (1.f - sg));
-    }
-    gp[i] = v;
+    const float pre = conv_at<KC>(wv, xw + i, bs);
+    const float sg = sigmoid_f(pre);
+    gp[i] = dvalid ? gp[i] * sg * fmaf(pre, 1.f - sg, 1.f) : 0.f;
   }
   float dwp[KC], dbp = 0.f;
 #pragma unroll
@@ -122,7 +151,7 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < KC; ++j) acc = fmaf(wv[j], gp[i + (KC - 1) - j], acc);
-    if (dvalid && p < g.L) dx[dxb + token_row(tok, p, g.L) * g.dxst + d] = acc;
+    if (dvalid && p < g.L) dxb[row_of<TOK>(tok, p, g.L) * g.dxst] = acc;
     // dw[j] += dpre[p] * x[p - (KC-1) + j]; db += dpre[p]
 #pragma unroll
     for (int j = 0; j < KC; ++j) dwp[j] = fmaf(gp[i], xw[i + j], dwp[j]);
@@ -142,20 +171,32 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
 }
 
 // dw (K, D, KC) and dbias (K, D): fixed-order float64 sum of the partials.
+// A block covers 64 consecutive (k, d, j) columns; its 4 waves each sum a
+// quarter of the partials, and the quarters are added in wave order.
 __global__ void __launch_bounds__(kThreads)
 conv_reduce_kernel(ConvGeom g, int kc, int64_t nparts, const float* __restrict__ part,
                    float* __restrict__ dw, float* __restrict__ db) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t total = g.K * g.D * (kc + 1);
-  if (idx >= total) return;
-  const int j = static_cast<int>(idx % (kc + 1));
-  const int64_t kd = idx / (kc + 1);
+  __shared__ double sq[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t ncol = g.K * g.D * (kc + 1);
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const int64_t colc = col < ncol ? col : 0;
+  const int64_t per = (nparts + 3) / 4;
+  const int64_t q0 = wave * per, q1 = min(nparts, q0 + per);
   double s = 0.0;
-  for (int64_t q = 0; q < nparts; ++q) s += part[(q * g.K * g.D + kd) * (kc + 1) + j];
-  if (j < kc)
-    dw[kd * kc + j] = static_cast<float>(s);
-  else
-    db[kd] = static_cast<float>(s);
+  for (int64_t q = q0; q < q1; ++q) s += part[q * ncol + colc];
+  sq[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && col < ncol) {
+    const double t = (sq[0][lane] + sq[1][lane]) + (sq[2][lane] + sq[3][lane]);
+    const int j = static_cast<int>(col % (kc + 1));
+    const int64_t kd = col / (kc + 1);
+    if (j < kc)
+      dw[kd * kc + j] = static_cast<float>(t);
+    else
+      db[kd] = static_cast<float>(t);
+  }
 }
 
 template <int KC>
@@ -163,7 +204,10 @@ static hipError_t conv_fwd_t(const ConvGeom& g, const float* x, const float* w, 
                              float* y, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((g.D + 63) / 64), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>((g.L + kCvBlockPos - 1) / kCvBlockPos));
-  hipLaunchKernelGGL((conv_fwd_kernel<KC>), grid, dim3(kThreads), 0, s, g, x, w, b, y);
+  if (g.tok)
+    hipLaunchKernelGGL((conv_fwd_kernel<KC, true>), grid, dim3(kThreads), 0, s, g, x, w, b, y);
+  else
+    hipLaunchKernelGGL((conv_fwd_kernel<KC, false>), grid, dim3(kThreads), 0, s, g, x, w, b, y);
   return hipGetLastError();
 }
 
@@ -173,9 +217,12 @@ static hipError_t conv_bwd_t(const ConvGeom& g, const float* x, const float* w, 
                              hipStream_t s) {
   const unsigned nz = static_cast<unsigned>((g.L + kCvBlockPos - 1) / kCvBlockPos);
   const dim3 grid(static_cast<unsigned>((g.D + 63) / 64), static_cast<unsigned>(g.B * g.K), nz);
-  hipLaunchKernelGGL((conv_bwd_kernel<KC>), grid, dim3(kThreads), 0, s, g, x, w, b, dy, dx, part);
+  if (g.tok)
+    hipLaunchKernelGGL((conv_bwd_kernel<KC, true>), grid, dim3(kThreads), 0, s, g, x, w, b, dy, dx, part);
+  else
+    hipLaunchKernelGGL((conv_bwd_kernel<KC, false>), grid, dim3(kThreads), 0, s, g, x, w, b, dy, dx, part);
   const int64_t total = g.K * g.D * (KC + 1);
-  hipLaunchKernelGGL(conv_reduce_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+  hipLaunchKernelGGL(conv_reduce_kernel, dim3(static_cast<unsigned>((total + 63) / 64)),
                      dim3(kThreads), 0, s, g, KC, g.B * static_cast<int64_t>(nz), part, dw, db);
   return hipGetLastError();
 }

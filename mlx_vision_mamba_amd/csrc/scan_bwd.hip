@@ -487,44 +487,66 @@ reduce_bc_kernel(Geom gm, BwdBufs bf) {
   const int64_t t = (idx / (2 * kStatePad)) % gm.L;
   const int64_t bk = idx / (2 * kStatePad * gm.L);
   if (n >= gm.N) return;
+  // the channel-block partials are summed left to right; unrolled so that
+  // their loads are in flight together
+  const float* pp = bf.part_bc + (bk * gm.ncblk * gm.L + t) * (2 * kStatePad) + w2 * kStatePad + n;
+  const int64_t cstride = gm.L * 2 * kStatePad;
   float s = 0.f;
-  for (int64_t cb = 0; cb < gm.ncblk; ++cb)
-    s += bf.part_bc[((bk * gm.ncblk + cb) * gm.L + t) * (2 * kStatePad) + w2 * kStatePad + n];
+#pragma unroll 4
+  for (int64_t cb = 0; cb < gm.ncblk; ++cb) s += pp[cb * cstride];
   const int64_t b = bk / gm.K, k = bk % gm.K;
   const int64_t row = token_row(gm.tok ? gm.tok + k * gm.L : nullptr, t, gm.L);
   OT* out = static_cast<OT*>(w2 ? bf.dC : bf.dB);
   st(out, b * gm.bsb + k * gm.bsk + row * gm.bst + n, s);
 }
 
-// dA (K, D, N) and dD (K, D): sum per-(b, chunk) partials in a fixed order
-// (mamba_metal_fused.py:214,218).
+// dA (K, D, N), dD (K, D) and (fused, when requested) the dt_bias gradient
+// (K, D): sum the per-(b, chunk) float64 partials in a fixed order
+// (mamba_metal_fused.py:214,218).  A block covers 64 consecutive output
+// columns; its 4 waves each sum a quarter of the B * nchunk partials and
+// the quarters are added in wave order.
 __global__ void __launch_bounds__(kThreads)
 reduce_ad_kernel(Geom gm, BwdBufs bf) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  __shared__ double sq[4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t nA = gm.K * gm.D * kStatePad;
-  if (idx < nA) {
-    const int n = static_cast<int>(idx % kStatePad);
-    const int64_t d = (idx / kStatePad) % gm.D;
-    const int64_t k = idx / (kStatePad * gm.D);
-    if (n >= gm.N) return;
-    double s = 0.0;
-    for (int64_t b = 0; b < gm.B; ++b)
-      for (int64_t c = 0; c < gm.nchunk; ++c)
-        s += bf.part_dA[(((b * gm.K + k) * gm.nchunk + c) * gm.D + d) * kStatePad + n];
-    bf.dA[(k * gm.D + d) * gm.N + n] = static_cast<float>(s);
-  } else if (idx < nA + 2 * gm.K * gm.D) {
-    // dD, then (fused, when requested) the dt_bias gradient
-    const bool is_db = idx >= nA + gm.K * gm.D;
-    if (is_db && bf.ddbias == nullptr) return;
-    const int64_t i = idx - nA - (is_db ? gm.K * gm.D : 0);
-    const int64_t d = i % gm.D;
-    const int64_t k = i / gm.D;
-    const double* part = is_db ? bf.part_db : bf.part_dD;
-    double s = 0.0;
-    for (int64_t b = 0; b < gm.B; ++b)
-      for (int64_t c = 0; c < gm.nchunk; ++c)
-        s += part[((b * gm.K + k) * gm.nchunk + c) * gm.D + d];
-    (is_db ? bf.ddbias : bf.dD)[k * gm.D + d] = static_cast<float>(s);
+  const int64_t nKD = gm.K * gm.D;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  int kind = 0;  // 0: dA, 1: dD, 2: dt_bias
+  int64_t k = 0, d = 0;
+  int n = 0;
+  if (col < nA) {
+    n = static_cast<int>(col % kStatePad);
+    d = (col / kStatePad) % gm.D;
+    k = col / (kStatePad * gm.D);
+  } else {
+    kind = col < nA + nKD ? 1 : 2;
+    const int64_t i = col - nA - (kind == 2 ? nKD : 0);
+    d = i % gm.D;
+    k = i / gm.D;
+  }
+  const bool valid = col < nA + 2 * nKD && (kind != 0 || n < gm.N) &&
+                     (kind != 2 || bf.ddbias != nullptr);
+  const int64_t nparts = gm.B * gm.nchunk;
+  const int64_t per = (nparts + 3) / 4;
+  const int64_t q0 = wave * per, q1 = min(nparts, q0 + per);
+  double s = 0.0;
+  if (valid) {
+    for (int64_t q = q0; q < q1; ++q) {
+      const int64_t b = q / gm.nchunk, c = q - (q / gm.nchunk) * gm.nchunk;
+      const int64_t slot = ((b * gm.K + k) * gm.nchunk + c) * gm.D + d;
+      s += kind == 0 ? bf.part_dA[slot * kStatePad + n] : (kind == 1 ? bf.part_dD[slot] : bf.part_db[slot]);
+    }
+  }
+  sq[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && valid) {
+    const float t = static_cast<float>((sq[0][lane] + sq[1][lane]) + (sq[2][lane] + sq[3][lane]));
+    if (kind == 0)
+      bf.dA[(k * gm.D + d) * gm.N + n] = t;
+    else
+      (kind == 1 ? bf.dD : bf.ddbias)[k * gm.D + d] = t;
   }
 }
 
@@ -546,7 +568,7 @@ static hipError_t launch_bwd_t(const Geom& g, const BwdBufs& b, hipStream_t s) {
   hipLaunchKernelGGL((reduce_bc_kernel<OT>), dim3(static_cast<unsigned>((nbc + kThreads - 1) / kThreads)),
                      block, 0, s, g, b);
   const int64_t nad = g.K * g.D * (kStatePad + 2);
-  hipLaunchKernelGGL(reduce_ad_kernel, dim3(static_cast<unsigned>((nad + kThreads - 1) / kThreads)),
+  hipLaunchKernelGGL(reduce_ad_kernel, dim3(static_cast<unsigned>((nad + 63) / 64)),
                      block, 0, s, g, b);
   return hipGetLastError();
 }
