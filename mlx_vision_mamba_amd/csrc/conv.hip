@@ -28,15 +28,6 @@ constexpr int kCvBlockPos = 64;   // positions per block
 // channel is out of range: no load sits behind a divergent branch, so the
 // window's loads issue back to back instead of waiting one by one.
 template <bool TOK>
-__device__ __forceinline__ int64_t row_of(const int32_t* tok, int64_t p, int64_t L) {
-  if constexpr (TOK) {
-    const int64_t r = ((const const_i32*)tok)[p];
-    return r < 0 ? 0 : (r >= L ? L - 1 : r);
-  } else {
-    return p;
-  }
-}
-template <bool TOK>
 __device__ __forceinline__ int64_t safe_row(const int32_t* tok, int64_t p, int64_t L) {
   return row_of<TOK>(tok, p < 0 ? 0 : (p >= L ? L - 1 : p), L);
 }

@@ -48,7 +48,7 @@ namespace mvm {
 
 // Pass 1: adjoint aggregate of chunks 1..nchunk-1: the mu that leaves the
 // chunk's first position when mu = 0 enters its last, and sum(delta).
-template <typename XT, bool FUSE>
+template <typename XT, bool FUSE, bool TOK>
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   __shared__ float sD[2][kSub][kChPerBlock];
@@ -61,21 +61,22 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int cl = wave * kChPerWave + (lane >> 2);
   const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
   const int64_t d = ch0 + cl;
-  const int64_t dld = ch0 + (tid & 63);
+  const int64_t dld = ch0 + lane;
   const bool dvalid = d < gm.D;
+  const bool cok = dld < gm.D;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
   const int64_t chunk = blockIdx.z + 1;
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
-  const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t drow = b * gm.dsb + k * gm.dsk;
-  const int64_t yrow = b * gm.ysb + k * gm.ysk;
+  const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
+  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;
+  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
   const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
   const XT* __restrict__ dy = static_cast<const XT*>(bf.dy);
-  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   auto stage_delta = [&](float (&v)[4]) {
     if (FUSE) {
 #pragma unroll
@@ -83,7 +84,7 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
     }
   };
   // fused gate: the scan's upstream gradient is dy * silu(z)
-  const int64_t zrow = b * gm.zsb + k * gm.zsk;
+  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;
   const bool gate = FUSE && bf.z != nullptr;
   float pz[4] = {0.f, 0.f, 0.f, 0.f};
   auto stage_g = [&](float (&gv)[4]) {
@@ -103,32 +104,29 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   float dsum = 0.f;
   const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pd[4], pg[4], pc;
-  {
-    const int64_t ts = t0 + (ntile - 1) * kSub;
-    const int nt = static_cast<int>(t1 - ts);
-    load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, ts, nt, gm.L, tid);
-    load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
-    if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
-    pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+  auto load_tile = [&](int64_t ts) {
+    const TileRows rows = tile_rows<TOK>(tok, ts, gm.L, tid);
+    load_xtile(pd, bf.delta, dbase, rows, gm.dst, lane, cok);
+    load_xtile(pg, dy, ybase, rows, gm.yst, lane, cok);
+    if (gate) load_xtile(pz, bf.z, zbase, rows, gm.zst, lane, cok);
+    pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
+  };
+  auto store_tile = [&](int buf) {
     stage_delta(pd);
     stage_g(pg);
-    store_xtile(sD[0], pd, tid);
-    store_xtile(sG[0], pg, tid);
-    sC[0][tid >> 4][tid & 15] = pc;
-  }
+    store_xtile(sD[buf], pd, tid);
+    store_xtile(sG[buf], pg, tid);
+    sC[buf][stile_row(tid)][tid & 15] = pc;
+  };
+  load_tile(t0 + (ntile - 1) * kSub);
+  store_tile(0);
   for (int64_t j = 0; j < ntile; ++j) {
     const int buf = static_cast<int>(j & 1);
     const int64_t ts = t0 + (ntile - 1 - j) * kSub;
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
     __syncthreads();
     const bool more = j + 1 < ntile;
-    if (more) {
-      const int64_t tn = ts - kSub;
-      load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
-      if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, tn, kSub, gm.L, tid);
-      pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
-    }
+    if (more) load_tile(ts - kSub);
 #pragma unroll
     for (int tt = kSub - 1; tt >= 0; --tt) {
       if (tt < nt) {
@@ -144,13 +142,7 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
         dsum += dl;
       }
     }
-    if (more) {
-      stage_delta(pd);
-      stage_g(pg);
-      store_xtile(sD[buf ^ 1], pd, tid);
-      store_xtile(sG[buf ^ 1], pg, tid);
-      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
-    }
+    if (more) store_tile(buf ^ 1);
   }
   if (dvalid) {
     const int64_t slot = (bk * gm.nchunk + chunk) * gm.D + d;
@@ -187,8 +179,8 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
 
 // Pass 3: the reverse sweep.  Each 16-step tile is processed as two 8-step
 // halves (later half first), each restarted from its checkpoint, so the
-// register tile is 9 x 4 states + 8 x 4 decays and three waves fit per SIMD.
-template <typename XT, typename OT, bool FUSE>
+// register tile is 9 x 4 states + 8 x 4 decays.
+template <typename XT, typename OT, bool FUSE, bool TOK>
 __global__ void __launch_bounds__(kThreads, 2)
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
@@ -209,8 +201,9 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int cl = wave * kChPerWave + (lane >> 2);
   const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
   const int64_t d = ch0 + cl;
-  const int64_t dld = ch0 + (tid & 63);
+  const int64_t dld = ch0 + lane;
   const bool dvalid = d < gm.D;
+  const bool cok = dld < gm.D;
   const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
@@ -218,10 +211,11 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t chunk = blockIdx.z;
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
-  const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xrow = b * gm.xsb + k * gm.xsk;
-  const int64_t drow = b * gm.dsb + k * gm.dsk;
-  const int64_t yrow = b * gm.ysb + k * gm.ysk;
+  const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
+  // row-independent offsets (including the block's first channel)
+  const int64_t xbase = b * gm.xsb + k * gm.xsk + ch0;
+  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;
+  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -260,7 +254,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   };
   // fused: the dt bias of the channel this thread stages / flushes, and its
   // gradient summed over the rows this thread flushes
-  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   double dbacc = 0.0;
   auto stage_delta = [&](float (&v)[4]) {
     if (FUSE) {
@@ -271,41 +265,39 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // fused gate: the upstream dy is the gradient of y_raw * silu(z); the scan
   // consumes g = dy * silu(z) and dz = dy * y_raw * silu'(z) leaves from the
   // staging registers of the tile (rows ts + tt, tt = wave + 4r)
-  const int64_t zrow = b * gm.zsb + k * gm.zsk;
+  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;
   const bool gate = FUSE && bf.z != nullptr;
   float pz[4] = {0.f, 0.f, 0.f, 0.f}, pyr[4] = {0.f, 0.f, 0.f, 0.f};
-  auto stage_gate = [&](float (&gv)[4], int64_t ts, int nt) {
+  auto stage_gate = [&](float (&gv)[4], const TileRows& rows, int nt) {
     if (gate) {
-      const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+      const int wrow = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float sg = sigmoid_f(pz[r]);
         const float dzv = gv[r] * pyr[r] * (sg * fmaf(pz[r], 1.f - sg, 1.f));
         gv[r] *= pz[r] * sg;
         const int tt = wrow + 4 * r;
-        if (tt < nt && dld < gm.D) bf.dz[zrow + token_row(tok, ts + tt, gm.L) * gm.zst + dld] = dzv;
+        if (tt < nt && cok) bf.dz[zbase + static_cast<int64_t>(rows.r[r]) * gm.zst + lane] = dzv;
       }
     }
   };
-  // write back du / ddelta rows and this block's dB | dC partials of a tile
-  auto flush = [&](int buf, int64_t ts, int nt) {
-    const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lch = tid & 63;
+  // write back du / ddelta rows (token rows `rows`) and this block's dB | dC
+  // partials of a tile
+  auto flush = [&](int buf, const TileRows& rows, int64_t ts, int nt) {
+    const int wrow = __builtin_amdgcn_readfirstlane(wave);
     float dbt = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
-      if (tt < nt) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        if (dld < gm.D) {
-          st(du_out + (xrow + row * gm.xst + ch0), lch, sU[buf][tt][lch]);
-          float dd = sG[buf][tt][lch];
-          if (FUSE) {
-            dd *= softplus_grad_from_value(sD[buf][tt][lch]);
-            dbt += dd;
-          }
-          bf.ddelta[drow + row * gm.dst + dld] = dd;
+      if (tt < nt && cok) {
+        const int64_t row = rows.r[r];
+        st(du_out + (xbase + row * gm.xst), lane, sU[buf][tt][lane]);
+        float dd = sG[buf][tt][lane];
+        if (FUSE) {
+          dd *= softplus_grad_from_value(sD[buf][tt][lane]);
+          dbt += dd;
         }
+        bf.ddelta[dbase + row * gm.dst + lane] = dd;
       }
     }
     if (FUSE) dbacc += static_cast<double>(dbt);
@@ -386,27 +378,35 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pu[4], pd[4], pg[4], pb, pc;
   float4 pck0, pck1;  // checkpoints entering the two halves of the staged tile
-  {
-    const int64_t ts = t0 + (ntile - 1) * kSub;
-    const int nt = static_cast<int>(t1 - ts);
-    load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, ts, nt, gm.L, tid);
-    load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, ts, nt, gm.L, tid);
-    load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
+  auto load_tile = [&](const TileRows& rows, int64_t ts) {
+    load_xtile(pu, u, xbase, rows, gm.xst, lane, cok);
+    load_xtile(pd, bf.delta, dbase, rows, gm.dst, lane, cok);
+    load_xtile(pg, dy, ybase, rows, gm.yst, lane, cok);
     if (gate) {
-      load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
-      load_xtile(pyr, bf.y_raw, yrow, dld, gm.D, gm.yst, tok, ts, nt, gm.L, tid);
+      load_xtile(pz, bf.z, zbase, rows, gm.zst, lane, cok);
+      load_xtile(pyr, bf.y_raw, ybase, rows, gm.yst, lane, cok);
     }
-    pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
-    pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, ts, nt, gm.L, tid);
+    pb = load_stile(Bm, bcbase, rows, gm.bst, gm.N, tid);
+    pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
     pck0 = load_ckpt(ts);
     pck1 = load_ckpt(ts + kCk);
+  };
+  auto store_tile = [&](int buf, const TileRows& rows, int nt) {
     stage_delta(pd);
-    stage_gate(pg, ts, nt);
-    store_xtile(sU[0], pu, tid);
-    store_xtile(sD[0], pd, tid);
-    store_xtile(sG[0], pg, tid);
-    sB[0][tid >> 4][tid & 15] = pb;
-    sC[0][tid >> 4][tid & 15] = pc;
+    stage_gate(pg, rows, nt);
+    store_xtile(sU[buf], pu, tid);
+    store_xtile(sD[buf], pd, tid);
+    store_xtile(sG[buf], pg, tid);
+    sB[buf][stile_row(tid)][tid & 15] = pb;
+    sC[buf][stile_row(tid)][tid & 15] = pc;
+  };
+  TileRows rc, rp;  // rows of the tile being computed, of the one before it
+  {
+    const int64_t ts = t0 + (ntile - 1) * kSub;
+    rc = tile_rows<TOK>(tok, ts, gm.L, tid);
+    rp = rc;
+    load_tile(rc, ts);
+    store_tile(0, rc, static_cast<int>(t1 - ts));
   }
 
   for (int64_t j = 0; j < ntile; ++j) {
@@ -414,22 +414,13 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     const int64_t ts = t0 + (ntile - 1 - j) * kSub;
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
     __syncthreads();  // tile j staged; the previous tile's outputs are complete
-    if (j > 0) flush(buf ^ 1, ts + kSub, static_cast<int>(min<int64_t>(kSub, t1 - ts - kSub)));
+    if (j > 0) flush(buf ^ 1, rp, ts + kSub, static_cast<int>(min<int64_t>(kSub, t1 - ts - kSub)));
     const float4 hin0 = pck0, hin1 = pck1;
     const bool more = j + 1 < ntile;
+    TileRows rn = rc;
     if (more) {  // prefetch the previous tile (next in processing order)
-      const int64_t tn = ts - kSub;
-      load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pd, bf.delta, drow, dld, gm.D, gm.dst, tok, tn, kSub, gm.L, tid);
-      load_xtile(pg, dy, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
-      if (gate) {
-        load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, tn, kSub, gm.L, tid);
-        load_xtile(pyr, bf.y_raw, yrow, dld, gm.D, gm.yst, tok, tn, kSub, gm.L, tid);
-      }
-      pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
-      pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, kSub, gm.L, tid);
-      pck0 = load_ckpt(tn);
-      pck1 = load_ckpt(tn + kCk);
+      rn = tile_rows<TOK>(tok, ts - kSub, gm.L, tid);
+      load_tile(rn, ts - kSub);
     }
     // per-tile partial sums of dA / dD, folded into float64 once per tile
 #pragma unroll
@@ -447,17 +438,13 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     dDacc += static_cast<double>(tD);
     if (more) {
       __syncthreads();  // all flushes of the other buffer are done before it is refilled
-      stage_delta(pd);
-      stage_gate(pg, ts - kSub, kSub);
-      store_xtile(sU[buf ^ 1], pu, tid);
-      store_xtile(sD[buf ^ 1], pd, tid);
-      store_xtile(sG[buf ^ 1], pg, tid);
-      sB[buf ^ 1][tid >> 4][tid & 15] = pb;
-      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
+      store_tile(buf ^ 1, rn, kSub);
     }
+    rp = rc;
+    rc = rn;
   }
   __syncthreads();
-  flush(static_cast<int>((ntile - 1) & 1), t0, static_cast<int>(min<int64_t>(kSub, t1 - t0)));
+  flush(static_cast<int>((ntile - 1) & 1), rp, t0, static_cast<int>(min<int64_t>(kSub, t1 - t0)));
 
   if (dvalid) {
     double* pa = bf.part_dA + slot * kStatePad + 4 * grp;
@@ -550,20 +537,20 @@ reduce_ad_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
-template <typename XT, typename OT, bool FUSE = false>
-static hipError_t launch_bwd_t(const Geom& g, const BwdBufs& b, hipStream_t s) {
+template <typename XT, typename OT, bool FUSE, bool TOK>
+static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   const int64_t tot_state = g.B * g.K * g.D * kStatePad;
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE, TOK>), grid_agg, block, 0, s, g, b);
     hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3(static_cast<unsigned>((tot_state + kThreads - 1) / kThreads)),
                        block, 0, s, g, b);
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE>), grid, block, 0, s, g, b);
+  hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK>), grid, block, 0, s, g, b);
   const int64_t nbc = g.B * g.K * g.L * 2 * kStatePad;
   hipLaunchKernelGGL((reduce_bc_kernel<OT>), dim3(static_cast<unsigned>((nbc + kThreads - 1) / kThreads)),
                      block, 0, s, g, b);
@@ -571,6 +558,12 @@ static hipError_t launch_bwd_t(const Geom& g, const BwdBufs& b, hipStream_t s) {
   hipLaunchKernelGGL(reduce_ad_kernel, dim3(static_cast<unsigned>((nad + 63) / 64)),
                      block, 0, s, g, b);
   return hipGetLastError();
+}
+
+// remapped (seq_to_tok given) and identity-order instantiations
+template <typename XT, typename OT, bool FUSE = false>
+static hipError_t launch_bwd_t(const Geom& g, const BwdBufs& b, hipStream_t s) {
+  return g.tok ? launch_bwd_tt<XT, OT, FUSE, true>(g, b, s) : launch_bwd_tt<XT, OT, FUSE, false>(g, b, s);
 }
 
 hipError_t launch_bwd(const Geom& g, const BwdBufs& b, int in_dtype, int out_dtype, hipStream_t s) {

@@ -165,46 +165,76 @@ __device__ __forceinline__ float channel_reduce4(float v0, float v1, float v2, f
 
 // ------------------------------------------------------ tile staging
 // A tile is kSub consecutive scan positions of one workgroup's 64 channels.
-// Channel-indexed tensors are loaded fully coalesced: thread i holds scan
-// positions (i >> 6) + 4r, r = 0..3, of channel (i & 63), so every wave
-// reads 64 consecutive channels of one token row per instruction.
-// State-indexed tensors (B, C): thread i holds position i >> 4, state i & 15.
+// Wave w stages and writes back positions w + 4r (r = 0..3) of each tile:
+// for channel-indexed tensors lane l holds channel l of those rows (one load
+// instruction reads 64 consecutive channels of one token row); for
+// state-indexed tensors (B, C) lane l holds state l & 15 of row
+// w + 4 (l >> 4).  The 4 token rows of a wave are looked up once per tile
+// (wave-uniform, in SGPRs) and shared by every tensor staged or written
+// back for that tile.
 
-template <typename T>
-__device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ p, int64_t base,
-                                           int64_t ch, int64_t D, int64_t xst,
-                                           const int32_t* tok, int64_t ts, int nt, int64_t L,
-                                           int tid) {
-  // the row of each load is wave-uniform: keep its pointer in SGPRs and use
-  // a 32-bit per-lane channel offset
-  const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lch = tid & 63;
-  const bool cok = ch < D;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int tt = wrow + 4 * r;
-    v[r] = 0.f;
-    if (tt < nt) {
-      const T* rowp = p + (base + token_row(tok, ts + tt, L) * xst + (ch - lch));
-      if (cok) v[r] = to_f32(rowp[lch]);
-    }
+// Token row of scan position p in [0, L): the remap table entry clamped to
+// [0, L) (TOK), or p itself (identity order).  The table is read through the
+// constant address space: a wave-uniform lookup is a scalar load.
+template <bool TOK>
+__device__ __forceinline__ int32_t row_of(const int32_t* tok, int64_t p, int64_t L) {
+  if constexpr (TOK) {
+    const int32_t r = ((const const_i32*)tok)[p];
+    return r < 0 ? 0 : (r >= L ? static_cast<int32_t>(L - 1) : r);
+  } else {
+    return static_cast<int32_t>(p);
   }
 }
 
-template <typename T>
-__device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base, int64_t N,
-                                            int64_t bst, const int32_t* tok, int64_t ts, int nt,
-                                            int64_t L, int tid) {
-  // a wave covers 4 consecutive positions (16 lanes each): look their rows
-  // up with wave-uniform (scalar) loads, then pick this lane's quarter
-  const int tt = tid >> 4, n = tid & 15;
-  const int w4 = __builtin_amdgcn_readfirstlane(tid >> 6) * 4;
-  int64_t rows[4];
+struct TileRows {
+  int32_t r[4];  // token rows of positions ts + wave + 4r
+};
+
+// Rows of a wave's 4 positions of the tile starting at ts.  Positions past
+// L are clamped to L - 1: their values are staged but never used.
+template <bool TOK>
+__device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int64_t ts, int64_t L, int tid) {
+  const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+  TileRows t;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) rows[q] = (w4 + q < nt) ? token_row(tok, ts + w4 + q, L) : 0;
-  const int q = tt & 3;
-  const int64_t row = q == 0 ? rows[0] : (q == 1 ? rows[1] : (q == 2 ? rows[2] : rows[3]));
-  return (tt < nt && n < N) ? ld(p, base + row * bst + n) : 0.f;
+  for (int r = 0; r < 4; ++r) {
+    const int64_t p = ts + wrow + 4 * r;
+    t.r[r] = row_of<TOK>(tok, p < L ? p : L - 1, L);
+  }
+  return t;
+}
+
+// Channel-indexed tile rows: v[r] = p[base + rows.r[r] * st + lane] (base
+// includes the block's first channel).  Out-of-range channels (cok false)
+// read channel 0 of the row, always in bounds, and yield 0: no load waits
+// behind a divergent branch.
+template <typename T>
+__device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ p, int64_t base,
+                                           const TileRows& rows, int64_t st, int lch, bool cok) {
+  const int lc = cok ? lch : 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const T* rowp = p + (base + static_cast<int64_t>(rows.r[r]) * st);  // SGPR pointer
+    const float x = to_f32(rowp[lc]);
+    v[r] = cok ? x : 0.f;
+  }
+}
+
+// LDS row of the state-indexed value a thread stages (row w + 4 (l >> 4)).
+__device__ __forceinline__ int stile_row(int tid) { return (tid >> 6) + 4 * ((tid >> 4) & 3); }
+
+// State-indexed tile value of this thread: state tid & 15 of row
+// stile_row(tid); states >= N yield 0.
+template <typename T>
+__device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base,
+                                            const TileRows& rows, int64_t st, int64_t N, int tid) {
+  const int q = (tid >> 4) & 3, n = tid & 15;
+  const int64_t o0 = static_cast<int64_t>(rows.r[0]) * st, o1 = static_cast<int64_t>(rows.r[1]) * st;
+  const int64_t o2 = static_cast<int64_t>(rows.r[2]) * st, o3 = static_cast<int64_t>(rows.r[3]) * st;
+  const int64_t off = q == 0 ? o0 : (q == 1 ? o1 : (q == 2 ? o2 : o3));
+  const bool nok = n < N;
+  const float x = ld(p, base + off + (nok ? n : 0));
+  return nok ? x : 0.f;
 }
 
 __device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float (&v)[4], int tid) {

@@ -40,7 +40,7 @@ namespace mvm {
 
 enum FwdMode { kAgg = 0, kMain = 1 };
 
-template <typename XT, typename OT, int MODE, bool FUSE>
+template <typename XT, typename OT, int MODE, bool FUSE, bool TOK>
 __global__ void __launch_bounds__(kThreads, 6)
 scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // double-buffered tile staging: u, delta (64 channels), B, C (16 states);
@@ -58,8 +58,9 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int cl = wave * kChPerWave + (lane >> 2);          // compute channel within the block
   const int64_t ch0 = static_cast<int64_t>(blockIdx.x) * kChPerBlock;
   const int64_t d = ch0 + cl;
-  const int64_t dld = ch0 + (tid & 63);                    // channel this thread loads / stores
+  const int64_t dld = ch0 + lane;                          // channel this thread loads / stores
   const bool dvalid = d < gm.D;
+  const bool cok = dld < gm.D;
   const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
@@ -67,11 +68,12 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int64_t chunk = blockIdx.z;
   const int64_t t0 = chunk * gm.chunk_len;
   const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
-  const int32_t* tok = gm.tok ? gm.tok + k * gm.L : nullptr;
-  const int64_t xrow = b * gm.xsb + k * gm.xsk;            // + row * xst + channel
-  const int64_t drow = b * gm.dsb + k * gm.dsk;            // delta
-  const int64_t yrow = b * gm.ysb + k * gm.ysk;            // y, y_raw
-  const int64_t zrow = b * gm.zsb + k * gm.zsk;            // gate
+  const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
+  // row-independent offsets (including the block's first channel)
+  const int64_t xbase = b * gm.xsb + k * gm.xsk + ch0;     // u
+  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;     // delta
+  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;     // y, y_raw
+  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;     // gate
   const int64_t bcbase = b * gm.bsb + k * gm.bsk;
 
   const XT* __restrict__ u = static_cast<const XT*>(bf.u);
@@ -81,7 +83,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   OT* __restrict__ y = static_cast<OT*>(bf.y);
   float* __restrict__ ckpt = bf.ckpt;
   // fused prologue: the dt bias of the channel this thread stages
-  const float dbias_l = (FUSE && bf.dbias != nullptr && dld < gm.D) ? bf.dbias[k * gm.D + dld] : 0.f;
+  const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   const bool gate = FUSE && MODE == kMain && bf.z != nullptr;
   float* __restrict__ y_raw = FUSE ? bf.y_raw : nullptr;
 
@@ -104,22 +106,19 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // checkpoint slot s holds the state after position 8s + 7
   float* ckp = write_ck ? ckpt + (bk * gm.nck * gm.D + d) * kStatePad + 4 * grp : nullptr;
   const int64_t ck_stride = gm.D * kStatePad;
-  // y of a staged tile (held in sU) back to HBM; zv = the gate values of the
-  // same rows and channel when fused
-  auto flush_y = [&](int buf, int64_t ts, int nt, const float (&zv)[4]) {
-    const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lch = tid & 63;
+  // y of a staged tile (held in sU, token rows `rows`) back to HBM; zv = the
+  // gate values of the same rows and channel when fused
+  auto flush_y = [&](int buf, const TileRows& rows, int nt, const float (&zv)[4]) {
+    const int wrow = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
-      if (tt < nt) {
-        const int64_t row = token_row(tok, ts + tt, gm.L);
-        float v = sU[buf][tt][lch];
-        if (dld < gm.D) {
-          if (FUSE && y_raw != nullptr) y_raw[yrow + row * gm.yst + dld] = v;
-          if (gate) v *= zv[r] * sigmoid_f(zv[r]);
-          st(y + (yrow + row * gm.yst + ch0), lch, v);
-        }
+      if (tt < nt && cok) {
+        const int64_t roff = static_cast<int64_t>(rows.r[r]) * gm.yst;
+        float v = sU[buf][tt][lane];
+        if (FUSE && y_raw != nullptr) y_raw[ybase + roff + lane] = v;
+        if (gate) v *= zv[r] * sigmoid_f(zv[r]);
+        st(y + (ybase + roff), lane, v);
       }
     }
   };
@@ -158,38 +157,40 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   auto store_ck = [&](int64_t pos_end) {  // state after position pos_end (== 8s + 7)
     *reinterpret_cast<float4*>(ckp + (pos_end / kCk) * ck_stride) = make_float4(h[0], h[1], h[2], h[3]);
   };
+  auto load_tile = [&](const TileRows& rows, float (&pu)[4], float (&pd)[4], float& pb, float& pc) {
+    load_xtile(pu, u, xbase, rows, gm.xst, lane, cok);
+    load_xtile(pd, delta, dbase, rows, gm.dst, lane, cok);
+    pb = load_stile(Bm, bcbase, rows, gm.bst, gm.N, tid);
+    if (MODE == kMain) pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
+  };
+  auto store_tile = [&](int buf, const float (&pu)[4], const float (&pd)[4], float pb, float pc) {
+    store_xtile(sU[buf], pu, tid);
+    store_xtile(sD[buf], pd, tid);
+    sB[buf][stile_row(tid)][tid & 15] = pb;
+    sC[buf][stile_row(tid)][tid & 15] = pc;
+  };
 
   const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pu[4], pd[4], pz[4] = {0.f, 0.f, 0.f, 0.f}, pb = 0.f, pc = 0.f;
-  {
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - t0));
-    load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, t0, nt, gm.L, tid);
-    load_xtile(pd, delta, drow, dld, gm.D, gm.dst, tok, t0, nt, gm.L, tid);
-    pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
-    if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, t0, nt, gm.L, tid);
-    stage_delta(pd);
-    store_xtile(sU[0], pu, tid);
-    store_xtile(sD[0], pd, tid);
-    sB[0][tid >> 4][tid & 15] = pb;
-    sC[0][tid >> 4][tid & 15] = pc;
-  }
+  TileRows rc = tile_rows<TOK>(tok, t0, gm.L, tid);  // rows of the tile being computed
+  TileRows rp = rc;                                   // rows of the previous tile
+  load_tile(rc, pu, pd, pb, pc);
+  stage_delta(pd);
+  store_tile(0, pu, pd, pb, pc);
 
   for (int64_t it = 0; it < ntile; ++it) {
     const int buf = static_cast<int>(it & 1);
     const int64_t ts = t0 + it * kSub;
     const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
     __syncthreads();  // tile `it` staged; readers of the other buffer are done
-    if (write_y && it > 0) flush_y(buf ^ 1, ts - kSub, kSub, pz);
+    if (write_y && it > 0) flush_y(buf ^ 1, rp, kSub, pz);
     // gate values of this tile, used when it is flushed one tile later
-    if (gate) load_xtile(pz, bf.z, zrow, dld, gm.D, gm.zst, tok, ts, nt, gm.L, tid);
+    if (gate) load_xtile(pz, bf.z, zbase, rc, gm.zst, lane, cok);
     const bool more = it + 1 < ntile;
+    TileRows rn = rc;
     if (more) {  // prefetch the next tile; its latency overlaps this tile's math
-      const int64_t tn = ts + kSub;
-      const int ntn = static_cast<int>(min<int64_t>(kSub, t1 - tn));
-      load_xtile(pu, u, xrow, dld, gm.D, gm.xst, tok, tn, ntn, gm.L, tid);
-      load_xtile(pd, delta, drow, dld, gm.D, gm.dst, tok, tn, ntn, gm.L, tid);
-      pb = load_stile(Bm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
-      if (MODE == kMain) pc = load_stile(Cm, bcbase, gm.N, gm.bst, tok, tn, ntn, gm.L, tid);
+      rn = tile_rows<TOK>(tok, ts + kSub, gm.L, tid);
+      load_tile(rn, pu, pd, pb, pc);
     }
     if (nt == kSub) {  // full tile: no per-step bounds checks
 #pragma unroll
@@ -205,16 +206,15 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     }
     if (more) {
       stage_delta(pd);
-      store_xtile(sU[buf ^ 1], pu, tid);
-      store_xtile(sD[buf ^ 1], pd, tid);
-      sB[buf ^ 1][tid >> 4][tid & 15] = pb;
-      sC[buf ^ 1][tid >> 4][tid & 15] = pc;
+      store_tile(buf ^ 1, pu, pd, pb, pc);
     }
+    rp = rc;
+    rc = rn;
   }
   if (write_y) {
     __syncthreads();
     const int64_t ts = t0 + (ntile - 1) * kSub;
-    flush_y(static_cast<int>((ntile - 1) & 1), ts, static_cast<int>(t1 - ts), pz);
+    flush_y(static_cast<int>((ntile - 1) & 1), rp, static_cast<int>(t1 - ts), pz);
   }
 
   if (MODE == kAgg && dvalid) {
@@ -249,21 +249,27 @@ scan_fwd_carry_kernel(Geom gm, FwdBufs bf) {
   }
 }
 
-template <typename XT, typename OT, bool FUSE = false>
-static hipError_t launch_fwd_t(const Geom& g, const FwdBufs& b, hipStream_t s) {
+template <typename XT, typename OT, bool FUSE, bool TOK>
+static hipError_t launch_fwd_tt(const Geom& g, const FwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE, TOK>), grid_agg, block, 0, s, g, b);
     const int64_t total = g.B * g.K * g.D * kStatePad;
     hipLaunchKernelGGL(scan_fwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
                        block, 0, s, g, b);
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain, FUSE>), grid, block, 0, s, g, b);
+  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain, FUSE, TOK>), grid, block, 0, s, g, b);
   return hipGetLastError();
+}
+
+// remapped (seq_to_tok given) and identity-order instantiations
+template <typename XT, typename OT, bool FUSE = false>
+static hipError_t launch_fwd_t(const Geom& g, const FwdBufs& b, hipStream_t s) {
+  return g.tok ? launch_fwd_tt<XT, OT, FUSE, true>(g, b, s) : launch_fwd_tt<XT, OT, FUSE, false>(g, b, s);
 }
 
 hipError_t launch_fwd(const Geom& g, const FwdBufs& b, int in_dtype, int out_dtype, hipStream_t s) {
