@@ -289,15 +289,19 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
-      if (tt < nt && cok) {
+      if (tt < nt) {
+        // values first (no divergent branch); only the stores are masked
         const int64_t row = rows.r[r];
-        st(du_out + (xbase + row * gm.xst), lane, sU[buf][tt][lane]);
+        const float duv = sU[buf][tt][lane];
         float dd = sG[buf][tt][lane];
         if (FUSE) {
           dd *= softplus_grad_from_value(sD[buf][tt][lane]);
-          dbt += dd;
+          dbt += cok ? dd : 0.f;
         }
-        bf.ddelta[dbase + row * gm.dst + lane] = dd;
+        if (cok) {
+          st(du_out + (xbase + row * gm.xst), lane, duv);
+          bf.ddelta[dbase + row * gm.dst + lane] = dd;
+        }
       }
     }
     if (FUSE) dbacc += static_cast<double>(dbt);

@@ -74,11 +74,12 @@ __device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int6
 // log(1 + y) for y in (0, 1]: a 5-term series below 1/64 (truncation
 // < y^6 / 6 relative), else ln2 * log2(1 + y) (the rounding of 1 + y is
 // < 2^-24 absolute, < 2e-6 relative there).
+// Both branches are evaluated and selected (no divergent control flow).
 __device__ __forceinline__ float log1p_unit(float y) {
   constexpr float kLn2 = 0.6931471805599453f;
-  if (y < 0.015625f)
-    return y * fmaf(y, fmaf(y, fmaf(y, fmaf(y, 0.2f, -0.25f), 1.f / 3.f), -0.5f), 1.f);
-  return kLn2 * __builtin_amdgcn_logf(1.f + y);
+  const float series = y * fmaf(y, fmaf(y, fmaf(y, fmaf(y, 0.2f, -0.25f), 1.f / 3.f), -0.5f), 1.f);
+  const float direct = kLn2 * __builtin_amdgcn_logf(1.f + y);
+  return y < 0.015625f ? series : direct;
 }
 // softplus with torch.nn.functional's threshold (x > 20 -> x):
 // max(x, 0) + log(1 + e^-|x|)
@@ -94,9 +95,9 @@ __device__ __forceinline__ float sigmoid_f(float x) {
 // d softplus(x) / dx = sigmoid(x) = 1 - e^-sp from the softplus value sp >= 0
 // (series below 1/64, where 1 - e^-sp would cancel)
 __device__ __forceinline__ float softplus_grad_from_value(float sp) {
-  if (sp < 0.015625f)
-    return sp * fmaf(sp, fmaf(sp, fmaf(sp, -1.f / 24.f, 1.f / 6.f), -0.5f), 1.f);
-  return 1.f - __builtin_amdgcn_exp2f(-sp * kLog2e);
+  const float series = sp * fmaf(sp, fmaf(sp, fmaf(sp, -1.f / 24.f, 1.f / 6.f), -0.5f), 1.f);
+  const float direct = 1.f - __builtin_amdgcn_exp2f(-sp * kLog2e);
+  return sp < 0.015625f ? series : direct;
 }
 
 // 2^x on the transcendental unit (v_exp_f32); callers pre-scale by log2(e).
