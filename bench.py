@@ -9,7 +9,10 @@ batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
 384 (d_inner 768), d_state 16, depth 6, float32 random-init weights
 (Kaiming-uniform projections, S4D-real A, dt bias with softplus(bias) in
 [1e-3, 1e-1]); loss = mean of the output features; one step = forward +
-loss + backward + AdamW update (torch's fused AdamW).  Inputs are resident on the GPU before the
+loss + backward + AdamW update (torch's fused AdamW).  The fp32 projection
+GEMMs use the TunableOp picks recorded for this step on MI355X
+(mlx_vision_mamba_amd/tuning/, read-only; --default-gemms for the library
+defaults).  Inputs are resident on the GPU before the
 timed region; W untimed warm-up steps, then exactly K steps between two
 device synchronisations.  value = images / second.
 
@@ -252,9 +255,13 @@ def cpu_scan_baseline(torch):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tune-gemms", metavar="CSV", default=None,
+                    help="tune the step's GEMMs with TunableOp (2 steps) and write the picks to CSV")
+    ap.add_argument("--default-gemms", action="store_true",
+                    help="library-default GEMM selections (ignore the recorded MI355X picks)")
     ap.add_argument("--scan-driver", action="store_true",
                     help="profiling driver only: a 512 MiB copy + 2 scan fwd/VJP calls at the "
                          "VisionMamba step shape")
@@ -269,10 +276,18 @@ def main():
     import mlx_vision_mamba_amd as mvm
     from mlx_vision_mamba_amd import scan
 
+    from mlx_vision_mamba_amd import gemm_tuning
+
     device = torch.device("cuda:0")
     if args.scan_driver:
         scan_driver(torch, scan, device)
         return
+    if args.tune_gemms:
+        gemm_tuning.start_tuning(args.tune_gemms)
+        bench_step(torch, mvm, scan, 2, 1, device)
+        print(json.dumps({"tuned_gemms": args.tune_gemms}), flush=True)
+        return
+    tuned = False if args.default_gemms else gemm_tuning.load()
     elapsed, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
     imgs = 32 * args.steps / elapsed
 
@@ -307,6 +322,8 @@ def main():
                    "global_batch": 32, "image": "224x224x1", "patch": 16, "seq_len": 196,
                    "embed_dim": 384, "d_inner": 768, "d_state": 16, "depth": 6,
                    "directions": 4, "parallelism": "single GPU"},
+        "gemm_selection": ("TunableOp picks " + os.path.relpath(gemm_tuning.DEFAULT_FILE, ROOT)
+                           if tuned else "library default"),
         "roofline": roofline,
         "scan": scans,
     }
