@@ -40,10 +40,14 @@ def scan_sequential(x, delta, A, B, C, D):
     deltaA = torch.exp(delta_e * A[None, None])         # :52-53
     deltaBx = delta_e * B.unsqueeze(2) * x.unsqueeze(-1)  # :57-59
     h = x.new_zeros((bsz, d, n))                        # :62
+    # per-step views taken with one unbind: the same arithmetic as indexing
+    # [:, t], without autograd scattering every step's gradient into a
+    # full-size zero tensor
+    dA_t, dBx_t, C_t = deltaA.unbind(1), deltaBx.unbind(1), C.unbind(1)
     ys = []
     for t in range(L):                                  # :64
-        h = deltaA[:, t] * h + deltaBx[:, t]            # :65
-        ys.append((h * C[:, t].unsqueeze(1)).sum(-1))   # :67
+        h = dA_t[t] * h + dBx_t[t]                      # :65
+        ys.append((h * C_t[t].unsqueeze(1)).sum(-1))    # :67
     y = torch.stack(ys, dim=1)                          # :70
     return y + x * D                                    # :73
 
@@ -59,11 +63,13 @@ def scan_chunked(x, delta, A, B, C, D, chunk_size=32):
     parts = []
     for c0 in range(0, L, chunk_size):                    # :53
         c1 = min(c0 + chunk_size, L)
-        dA_c, dBx_c, C_c = deltaA[:, c0:c1], deltaBx[:, c0:c1], C[:, c0:c1]
+        dA_c = deltaA[:, c0:c1].unbind(1)
+        dBx_c = deltaBx[:, c0:c1].unbind(1)
+        C_c = C[:, c0:c1].unbind(1)
         ys = []
         for t in range(c1 - c0):                          # :64
-            h = dA_c[:, t] * h + dBx_c[:, t]
-            ys.append((h * C_c[:, t].unsqueeze(1)).sum(-1))
+            h = dA_c[t] * h + dBx_c[t]
+            ys.append((h * C_c[t].unsqueeze(1)).sum(-1))
         parts.append(torch.stack(ys, dim=1))              # :70
     return torch.cat(parts, dim=1) + x * D                # :73-74
 
