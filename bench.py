@@ -27,7 +27,8 @@ reads for a 512 MiB copy (committed summary in profiles/, made with
 `bench.py --scan-driver`), or null when that summary is absent.
 
 scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
-D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads.
+D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads,
+timed over back-to-back calls with inputs resident in HBM.
 
 cpu_baseline: the oracle's CPU restatement of the reference's sequential
 VisionMamba step (materialised discretisation, Python time loop, autograd)
@@ -49,8 +50,8 @@ if ROOT not in sys.path:
 
 METRIC = "selective-scan fwd+VJP GB/s & % HBM peak; VisionMamba-2D train imgs/sec"
 HBM_PEAK_GBS = 8000.0
-BWD_KERNELS = ("mvm_scan_fused_bwd: scan_bwd_kernel<float, float, fused> + reduce_bc_kernel + "
-               "reduce_ad_kernel (one time chunk at this shape, so no agg / carry pass)")
+BWD_KERNELS = ("mvm_scan_fused_bwd: scan_bwd_kernel<float, float, fused> + reduce_grads_kernel "
+               "(one time chunk at this shape, so no aggregate pass)")
 
 
 def _seeded_model(torch, mvm, device):
@@ -103,19 +104,19 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
         y, ck = scan.scan_forward(*args, save_ckpt=True)
         scan.scan_backward(*args, g4, ckpt=ck)
     torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    tf = tb = 0.0
-    for _ in range(iters):
-        evs[0].record()
+    # back-to-back calls (no synchronisation inside the timed loop): events
+    # before each forward and each VJP split the stream time between them
+    ev_f = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        ev_f[i].record()
         y, ck = scan.scan_forward(*args, save_ckpt=True)
-        evs[1].record()
+        ev_b[i].record()
         scan.scan_backward(*args, g4, ckpt=ck)
-        evs[2].record()
-        torch.cuda.synchronize()
-        tf += evs[0].elapsed_time(evs[1]) * 1e-3
-        tb += evs[1].elapsed_time(evs[2]) * 1e-3
-    tf /= iters
-    tb /= iters
+    ev_f[iters].record()
+    torch.cuda.synchronize()
+    tf = sum(ev_f[i].elapsed_time(ev_b[i]) for i in range(iters)) * 1e-3 / iters
+    tb = sum(ev_b[i].elapsed_time(ev_f[i + 1]) for i in range(iters)) * 1e-3 / iters
     size = 2 if dtype == torch.bfloat16 else 4
     bf, bb = scan.algorithmic_bytes(bsz, L, D, N, size, size)
     total = tf + tb
@@ -309,7 +310,7 @@ def main():
                      "algorithmic_bytes_per_launch": int(fwd_b)},
     }
     scans = {
-        "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 50, device),
+        "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 200, device),
         "long_B8_L16384_bf16": bench_scan(torch, scan, 8, 16384, 1536, 16, torch.bfloat16, 5, device),
     }
     out = {

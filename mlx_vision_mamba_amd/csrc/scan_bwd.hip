@@ -23,13 +23,15 @@
 //
 // Reductions are atomic-free and in a fixed order (bitwise deterministic):
 //   dB, dC   sum over 16 channels per wave with cross-lane ops, over the 4
-//            waves in LDS, then over channel blocks in reduce_bc_kernel;
+//            waves in LDS, then over channel blocks in reduce_grads_kernel;
 //   dA, dD   per-lane float32 sums over each 16-step tile, folded into
 //            float64 running sums (a long chunk of unit-size terms can
 //            cancel to ~1e-3, far below float32 running-sum error), float64
-//            partials per (b, chunk), summed in float64 by reduce_ad_kernel.
+//            partials per (b, chunk), summed in float64 by reduce_grads_kernel.
 // Long sequences: the adjoint carry between time chunks uses the same
-// two-pass idea as the forward, run right to left (bwd_agg + bwd_carry).
+// two-pass idea as the forward, run right to left: scan_bwd_agg_kernel
+// writes each chunk's adjoint aggregate; they are folded by each chunk of
+// the sweep itself (up to kFoldMax chunks) or by scan_bwd_carry_kernel.
 //
 // Fused form (FUSE, float32): delta = softplus(delta_raw + dt_bias) is
 // applied as the delta tile is staged; the stored gradient is that of
@@ -152,8 +154,8 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
-// Pass 2: fold adjoint aggregates right to left; agg_mu[c] becomes the mu
-// entering chunk c's last position.
+// Carry pass for many chunks: agg_mu[c] becomes the adjoint entering chunk
+// c's last position, folded right to left, one thread per (b, k, d, n).
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -177,10 +179,10 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
-// Pass 3: the reverse sweep.  Each 16-step tile is processed as two 8-step
+// Pass 2: the reverse sweep.  Each 16-step tile is processed as two 8-step
 // halves (later half first), each restarted from its checkpoint, so the
 // register tile is 9 x 4 states + 8 x 4 decays.
-template <typename XT, typename OT, bool FUSE, bool TOK>
+template <typename XT, typename OT, bool FUSE, bool TOK, bool FOLD>
 __global__ void __launch_bounds__(kThreads, 2)
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
@@ -236,8 +238,22 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     dacc[j] = 0.0;
   }
   if (chunk + 1 < gm.nchunk && dvalid) {
-    const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + slot * kStatePad + 4 * grp);
-    mu[0] = m4.x; mu[1] = m4.y; mu[2] = m4.z; mu[3] = m4.w;
+    if constexpr (FOLD) {
+      // adjoint carry-in: fold the aggregates of chunks nchunk-1 .. chunk+1
+      // right to left, mu = exp(A * S_c) * mu + M_c
+      const int64_t s0 = bk * gm.nchunk * gm.D + dc;
+      for (int64_t c = gm.nchunk - 1; c > chunk; --c) {
+        const int64_t sc = s0 + c * gm.D;
+        const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + sc * kStatePad + 4 * grp);
+        const float sd = bf.agg_s[sc];
+        const float m[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sd), mu[j], m[j]);
+      }
+    } else {  // folded by scan_bwd_carry_kernel
+      const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + slot * kStatePad + 4 * grp);
+      mu[0] = m4.x; mu[1] = m4.y; mu[2] = m4.z; mu[3] = m4.w;
+    }
   }
   const float dskip = dvalid ? bf.Dv[k * gm.D + d] : 0.f;
   double dDacc = 0.0;
@@ -467,10 +483,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 
 // dB / dC: sum the channel-block partials in a fixed order and store at the
 // token row each scan position read (mamba_metal_fused.py:221,224).
+// The two fixed-order reductions after the sweep, in one launch: blocks
+// [0, nbc_blocks) reduce dB / dC, the rest dA, dD and the dt bias.
+//
+// dB / dC: sum the channel-block partials in a fixed order and store at the
+// token row each scan position read (mamba_metal_fused.py:221,224).
 template <typename OT>
-__global__ void __launch_bounds__(kThreads)
-reduce_bc_kernel(Geom gm, BwdBufs bf) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+__device__ __forceinline__ void reduce_bc_part(const Geom& gm, const BwdBufs& bf, int64_t blk) {
+  const int64_t idx = blk * kThreads + threadIdx.x;
   const int64_t total = gm.B * gm.K * gm.L * 2 * kStatePad;
   if (idx >= total) return;
   const int n = static_cast<int>(idx % kStatePad);
@@ -496,14 +516,13 @@ reduce_bc_kernel(Geom gm, BwdBufs bf) {
 // (mamba_metal_fused.py:214,218).  A block covers 64 consecutive output
 // columns; its 4 waves each sum a quarter of the B * nchunk partials and
 // the quarters are added in wave order.
-__global__ void __launch_bounds__(kThreads)
-reduce_ad_kernel(Geom gm, BwdBufs bf) {
-  __shared__ double sq[4][64];
+__device__ __forceinline__ void reduce_ad_part(const Geom& gm, const BwdBufs& bf, int64_t blk,
+                                               double (*sq)[64]) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t nA = gm.K * gm.D * kStatePad;
   const int64_t nKD = gm.K * gm.D;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const int64_t col = blk * 64 + lane;
   int kind = 0;  // 0: dA, 1: dD, 2: dt_bias
   int64_t k = 0, d = 0;
   int n = 0;
@@ -541,26 +560,42 @@ reduce_ad_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
+template <typename OT>
+__global__ void __launch_bounds__(kThreads)
+reduce_grads_kernel(Geom gm, BwdBufs bf, int64_t nbc_blocks) {
+  __shared__ double sq[4][64];
+  const int64_t blk = blockIdx.x;
+  if (blk < nbc_blocks)
+    reduce_bc_part<OT>(gm, bf, blk);
+  else
+    reduce_ad_part(gm, bf, blk - nbc_blocks, sq);  // block-uniform branch: its barrier is safe
+}
+
 template <typename XT, typename OT, bool FUSE, bool TOK>
 static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
-  const int64_t tot_state = g.B * g.K * g.D * kStatePad;
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
     hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE, TOK>), grid_agg, block, 0, s, g, b);
-    hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3(static_cast<unsigned>((tot_state + kThreads - 1) / kThreads)),
-                       block, 0, s, g, b);
+    if (g.nchunk > kFoldMax) {
+      const int64_t total = g.B * g.K * g.D * kStatePad;
+      hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                         block, 0, s, g, b);
+    }
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK>), grid, block, 0, s, g, b);
-  const int64_t nbc = g.B * g.K * g.L * 2 * kStatePad;
-  hipLaunchKernelGGL((reduce_bc_kernel<OT>), dim3(static_cast<unsigned>((nbc + kThreads - 1) / kThreads)),
-                     block, 0, s, g, b);
-  const int64_t nad = g.K * g.D * (kStatePad + 2);
-  hipLaunchKernelGGL(reduce_ad_kernel, dim3(static_cast<unsigned>((nad + 63) / 64)),
-                     block, 0, s, g, b);
+  // the in-sweep fold is a separate instantiation: the one-chunk and
+  // carry-pass kernels carry no code for it
+  if (g.nchunk > 1 && g.nchunk <= kFoldMax)
+    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, true>), grid, block, 0, s, g, b);
+  else
+    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, false>), grid, block, 0, s, g, b);
+  const int64_t nbc_blocks = (g.B * g.K * g.L * 2 * kStatePad + kThreads - 1) / kThreads;
+  const int64_t nad_blocks = (g.K * g.D * (kStatePad + 2) + 63) / 64;
+  hipLaunchKernelGGL((reduce_grads_kernel<OT>), dim3(static_cast<unsigned>(nbc_blocks + nad_blocks)),
+                     block, 0, s, g, b, nbc_blocks);
   return hipGetLastError();
 }
 

@@ -21,6 +21,10 @@ constexpr int kChPerWave = 16;
 constexpr int kChPerBlock = 64;
 constexpr int kStatePad = 16;     // states per channel in every internal buffer
 constexpr float kLog2e = 1.4426950408889634f;
+// Up to this many time chunks, each chunk of the main scan folds the chunk
+// aggregates it needs itself (one launch fewer); beyond it a separate carry
+// pass folds them once, so no block waits on a long chain of loads.
+constexpr int64_t kFoldMax = 8;
 
 struct bf16_t {
   uint16_t bits;

@@ -19,11 +19,12 @@
 // Long sequences are split into time chunks so that the grid fills the
 // chip (the two-pass scheme whose carry step the reference left as TODO at
 // mamba_metal_chunked.py:268-272):
-//   pass 1 (kAgg)    each chunk scans from h = 0 and writes its end state
-//                    and sum(delta) (the chunk's decay is exp(A*sum(delta)));
-//   pass 2 (carry)   one thread per (b, k, d, n) folds the aggregates in
-//                    order: H_c = exp(A*S_c) * H_{c-1} + e_c (mamba_fast.py:85-86);
-//   pass 3 (kMain)   each chunk rescans from its carry-in, writes y and,
+//   pass 1 (kAgg)    each chunk but the last scans from h = 0 and writes its
+//                    end state and sum(delta) (its decay is exp(A*sum(delta)));
+//   carry            H_c = exp(A*S_c) * H_{c-1} + e_c (mamba_fast.py:85-86):
+//                    folded by each chunk of the main pass itself for up to
+//                    kFoldMax chunks, by scan_fwd_carry_kernel beyond;
+//   pass 2 (kMain)   each chunk rescans from its carry-in, writes y and,
 //                    when training, the state after every 8th position
 //                    (the backward's checkpoints).
 //
@@ -97,8 +98,22 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const float dskip = (MODE == kMain && dvalid) ? bf.Dv[k * gm.D + d] : 0.f;
   const int64_t slot = (bk * gm.nchunk + chunk) * gm.D + dc;  // (bk, chunk, d)
   if (MODE == kMain && chunk > 0 && dvalid) {
-    const float4 c4 = *reinterpret_cast<const float4*>(bf.agg_h + slot * kStatePad + 4 * grp);
-    h[0] = c4.x; h[1] = c4.y; h[2] = c4.z; h[3] = c4.w;
+    if (gm.nchunk <= kFoldMax) {
+      // carry-in: fold the aggregates of chunks 0..chunk-1 left to right,
+      // H = exp(A * S_c) * H + E_c (mamba_fast.py:85-86)
+      const int64_t s0 = bk * gm.nchunk * gm.D + dc;
+      for (int64_t c = 0; c < chunk; ++c) {
+        const int64_t sc = s0 + c * gm.D;
+        const float4 e4 = *reinterpret_cast<const float4*>(bf.agg_h + sc * kStatePad + 4 * grp);
+        const float sd = bf.agg_s[sc];
+        const float e[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = fmaf(fast_exp2(a2[j] * sd), h[j], e[j]);
+      }
+    } else {  // folded by scan_fwd_carry_kernel
+      const float4 c4 = *reinterpret_cast<const float4*>(bf.agg_h + slot * kStatePad + 4 * grp);
+      h[0] = c4.x; h[1] = c4.y; h[2] = c4.z; h[3] = c4.w;
+    }
   }
   float dsum = 0.f;
   const bool write_y = MODE == kMain && y != nullptr;
@@ -224,8 +239,8 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   }
 }
 
-// Pass 2: fold chunk aggregates left to right; agg_h[c] becomes chunk c's
-// carry-in (the state after the last position of chunk c-1).
+// Carry pass for many chunks: agg_h[c] becomes chunk c's carry-in (the state
+// after the last position of chunk c-1), one thread per (b, k, d, n).
 __global__ void __launch_bounds__(kThreads)
 scan_fwd_carry_kernel(Geom gm, FwdBufs bf) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -256,9 +271,11 @@ static hipError_t launch_fwd_tt(const Geom& g, const FwdBufs& b, hipStream_t s) 
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
     hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE, TOK>), grid_agg, block, 0, s, g, b);
-    const int64_t total = g.B * g.K * g.D * kStatePad;
-    hipLaunchKernelGGL(scan_fwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
-                       block, 0, s, g, b);
+    if (g.nchunk > kFoldMax) {
+      const int64_t total = g.B * g.K * g.D * kStatePad;
+      hipLaunchKernelGGL(scan_fwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                         block, 0, s, g, b);
+    }
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));

@@ -104,8 +104,10 @@ def test_parity_single_block_shape(cuda):
     check_all(scan_inputs.make(2, 196, 1536, 16, seed=0), cuda)
 
 
+# (1, 200, 64, 16): 7 chunks of 32 (carries folded in the main pass) and 13
+# chunks of 16 (separate carry pass)
 @pytest.mark.parametrize("shape", [(1, 1, 8, 16), (2, 17, 5, 5), (3, 50, 100, 13), (2, 64, 64, 16),
-                                   (1, 33, 70, 1)])
+                                   (1, 33, 70, 1), (1, 200, 64, 16)])
 @pytest.mark.parametrize("chunk_len", [0, 16, 32, "whole"])
 def test_parity_shapes_and_chunkings(cuda, shape, chunk_len):
     print(f"case: shape={shape} chunk_len={chunk_len}", flush=True)
