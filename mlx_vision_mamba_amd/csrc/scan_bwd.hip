@@ -353,6 +353,9 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         hs[i + 1][jj] = fmaf(ea[i][jj], hs[i][jj], dxu * bv[jj]);
       }
     }
+    // the reverse loop reads its operands from LDS again rather than keeping
+    // the forward loop's copies live (fewer VGPRs, earlier LDS issue)
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = kCk - 1; i >= 0; --i) {
       if (kFull || i < n) {

@@ -23,6 +23,13 @@ halves of one buffer, so no slice / cat / elementwise pass is materialised.
 Activations between the projections are kept direction-major,
 (K, B*N, features), so the x_proj / dt_proj GEMMs batch over K without
 copies.
+
+The direction blocks' per-direction parameters (in_proj, conv1d, x_proj,
+dt_proj, A_log, D) are slices of one (K, ...) buffer per kind owned by the
+direction module, so the batched operands are views, not per-step
+concatenations; each buffer's gradient returns to the K parameters as its K
+slices.  The buffers are (re)built at the first forward and whenever a
+parameter stops being its slice (after ``.to()``, or a replaced parameter).
 """
 
 from __future__ import annotations
@@ -109,8 +116,9 @@ class BidirectionalMambaBlock(nn.Module):
     def forward(self, x):
         h = self.norm(x)
         tok = _cached_table(self._tables, 2, x.shape[1], None, x.device)
-        return x + _directional_forward([self.forward_mamba, self.backward_mamba], h, tok,
-                                        self.scan_mode)
+        blocks = [self.forward_mamba, self.backward_mamba]
+        return x + _directional_forward(blocks, h, tok, self.scan_mode,
+                                        _direction_stacks(self, blocks))
 
 
 class MultiDirectionalMambaBlock(nn.Module):
@@ -144,6 +152,7 @@ class MultiDirectionalMambaBlock(nn.Module):
         bsz, n, _ = x.shape
         h = self.norm(x)                                                       # :548
         expected = math.prod(self.grid_shape) if self.grid_shape is not None else n
+        stacks = _direction_stacks(self, list(self.mamba_blocks))
         if n != expected and self.num_directions > 2:                         # :554-559
             tok = _cached_table(self._tables, 2, n, None, x.device)
             blocks = [self.mamba_blocks[0], self.mamba_blocks[1]]
@@ -151,7 +160,63 @@ class MultiDirectionalMambaBlock(nn.Module):
             grid = self.grid_shape if self.num_directions > 2 else None
             tok = _cached_table(self._tables, self.num_directions, n, grid, x.device)
             blocks = list(self.mamba_blocks)
-        return x + _directional_forward(blocks, h, tok, self.scan_mode)       # :562-566
+        return x + _directional_forward(blocks, h, tok, self.scan_mode, stacks)  # :562-566
+
+
+# per-direction parameters stored as slices of one (K, ...) buffer per kind
+STACKED_PARAMS = ("in_proj.weight", "conv1d.weight", "conv1d.bias", "x_proj.weight",
+                  "dt_proj.weight", "dt_proj.bias", "A_log", "D")
+
+
+def _param(blk, path):
+    obj = blk
+    for part in path.split("."):
+        obj = getattr(obj, part)
+    return obj
+
+
+def _is_slice_of(p, buf, k):
+    return (p.device == buf.device and p.dtype == buf.dtype and p.shape == buf.shape[1:]
+            and p.is_contiguous()
+            and p.data_ptr() == buf.data_ptr() + k * buf.stride(0) * buf.element_size())
+
+
+def _direction_stacks(owner, blocks):
+    """The (K, ...) buffers whose k-th slices are the parameters of blocks[k],
+    one per name of STACKED_PARAMS, kept on ``owner``.  Rebuilt (values
+    copied from the current parameters, which then become slices of the new
+    buffers) when any parameter is not its slice."""
+    params = [[_param(b, name) for b in blocks] for name in STACKED_PARAMS]
+    bufs = owner.__dict__.get("_param_stacks")
+    if bufs is not None and all(_is_slice_of(p, buf, k) for buf, ps in zip(bufs, params)
+                                for k, p in enumerate(ps)):
+        return bufs
+    with torch.no_grad():
+        bufs = [torch.stack([p.detach() for p in ps], 0) for ps in params]
+        for buf, ps in zip(bufs, params):
+            for k, p in enumerate(ps):
+                p.data = buf[k]
+    owner.__dict__["_param_stacks"] = bufs
+    return bufs
+
+
+class _DirectionParams(torch.autograd.Function):
+    """(buffers..., parameters...) -> the buffers, differentiable w.r.t. the
+    parameters that are their slices: the backward hands each buffer's
+    gradient to its K parameters as K contiguous slices (no copy)."""
+
+    @staticmethod
+    def forward(ctx, nbuf, *tensors):
+        ctx.nbuf = nbuf
+        ctx.K = tensors[0].shape[0]
+        return tuple(t.view_as(t) for t in tensors[:nbuf])
+
+    @staticmethod
+    def backward(ctx, *grads):
+        out = [None] * (1 + ctx.nbuf)
+        for g in grads:
+            out += list(g.unbind(0)) if g is not None else [None] * ctx.K
+        return tuple(out)
 
 
 def _cached_table(cache, K, n, grid, device):
@@ -226,7 +291,8 @@ class _MambaCoreFn(torch.autograd.Function):
         d_dbc[..., :R] = torch.bmm(ddelta_raw, W_dt)
         dW_dt = torch.bmm(ddelta_raw.transpose(1, 2), dbc[..., :R])
         # x_proj: dbc = xc @ W_x^T; the scan's du joins through the GEMM's beta
-        dxc = torch.baddbmm(du, d_dbc, W_x)
+        # (in place: du is this backward's own buffer, so no copy of it is made)
+        dxc = du.baddbmm_(d_dbc, W_x)
         dW_x = torch.bmm(d_dbc.transpose(1, 2), xc)
         # conv + SiLU: dx lands in the first half of dxz
         dconv_w, dconv_b = conv_silu_backward_into(xb, conv_w, conv_b, _bnkd(dxc, bsz, n),
@@ -235,22 +301,26 @@ class _MambaCoreFn(torch.autograd.Function):
         return dxz, dconv_w, dconv_b, dW_x, dW_dt, db_dt, dA_log, dDv, None, None, None
 
 
-def _directional_forward(blocks, h, tok, scan_mode):
+def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
     """Run len(blocks) MambaBlocks on one (B, N, E) input, block k scanning
-    in the order of tok[k], and return the sum of their outputs."""
+    in the order of tok[k], and return the sum of their outputs.  ``stacks``:
+    the buffers of _direction_stacks whose leading slices hold the blocks'
+    parameters (None: a single block, whose parameters are used as views)."""
     K = len(blocks)
     b0 = blocks[0]
     bsz, n, _ = h.shape
     din, ns, R = b0.d_inner, b0.d_state, b0.dt_rank
-    W_in = torch.cat([blk.in_proj.weight for blk in blocks], 0) if K > 1 else b0.in_proj.weight
+    if stacks is None:
+        per = [_param(b0, name).unsqueeze(0) for name in STACKED_PARAMS]
+    else:
+        per = _DirectionParams.apply(len(stacks), *[buf[:K] for buf in stacks],
+                                     *[_param(b, name) for name in STACKED_PARAMS
+                                       for b in blocks])
+    W_in, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv = per
+    W_in = W_in.reshape(K * 2 * din, W_in.shape[-1])                          # (K*2D, E)
     xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165-167
-    conv_w = torch.cat([blk.conv1d.weight for blk in blocks], 0).view(K, din, b0.d_conv)
-    conv_b = torch.cat([blk.conv1d.bias for blk in blocks], 0).view(K, din)
-    W_x = torch.stack([blk.x_proj.weight for blk in blocks], 0)                # (K, R+2N, Din)
-    W_dt = torch.stack([blk.dt_proj.weight for blk in blocks], 0)              # (K, Din, R)
-    b_dt = torch.stack([blk.dt_proj.bias for blk in blocks], 0)                # (K, Din)
-    A_log = torch.stack([blk.A_log for blk in blocks], 0)                      # (K, Din, N)
-    Dv = torch.stack([blk.D for blk in blocks], 0)
+    conv_w = conv_w.reshape(K, din, b0.d_conv)                                 # (K, Din, d_conv)
+    # W_x (K, R+2N, Din), W_dt (K, Din, R), b_dt (K, Din), A_log (K, Din, N), Dv (K, Din)
     if tok is not None:
         tok = tok.to(h.device).contiguous()
     # the reference's "metal" mode is inference only (mamba_metal.py:230)

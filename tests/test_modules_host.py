@@ -79,3 +79,59 @@ def test_parameter_names_and_init():
     torch.testing.assert_close(-torch.exp(blk.A_log[0]), -torch.arange(1, 17, dtype=torch.float32))
     dt = F.softplus(blk.dt_proj.bias)
     assert float(dt.min()) >= 1e-3 * (1 - 1e-5) and float(dt.max()) <= 1e-1 * (1 + 1e-5)
+
+
+def test_direction_parameter_stacks_alias_and_rebuild():
+    """The K direction blocks' parameters become slices of one (K, ...)
+    buffer per kind with their values kept; a second call reuses the
+    buffers; a dtype change (parameters moved one by one) rebuilds them."""
+    torch.manual_seed(0)
+    m = mb.MultiDirectionalMambaBlock(d_model=16, d_state=4, num_directions=4, grid_shape=(2, 3))
+    blocks = list(m.mamba_blocks)
+    before = {n: p.detach().clone() for n, p in m.named_parameters()}
+    bufs = mb._direction_stacks(m, blocks)
+    assert len(bufs) == len(mb.STACKED_PARAMS)
+    for buf, name in zip(bufs, mb.STACKED_PARAMS):
+        assert buf.shape[0] == 4
+        for k, b in enumerate(blocks):
+            p = mb._param(b, name)
+            assert mb._is_slice_of(p, buf, k), name
+            assert torch.equal(buf[k], before[f"mamba_blocks.{k}.{name}"])
+    for n, p in m.named_parameters():
+        assert torch.equal(p, before[n]), n
+    assert mb._direction_stacks(m, blocks) is bufs
+    # an in-place update through a parameter lands in the buffer
+    with torch.no_grad():
+        blocks[2].A_log.add_(1.0)
+    assert torch.equal(bufs[mb.STACKED_PARAMS.index("A_log")][2], blocks[2].A_log)
+    m.double()
+    bufs2 = mb._direction_stacks(m, blocks)
+    assert bufs2 is not bufs and bufs2[0].dtype == torch.float64
+    assert all(mb._is_slice_of(mb._param(b, n), buf, k) for buf, n in zip(bufs2, mb.STACKED_PARAMS)
+               for k, b in enumerate(blocks))
+
+
+@pytest.mark.parametrize("K_used", [4, 2])
+def test_direction_params_route_gradients_to_slices(K_used):
+    """_DirectionParams returns the buffers (views, no copy) and hands each
+    buffer's gradient to the parameters as slices: for a loss sum(w * buf)
+    the gradient of block k's parameter is w[k]; with K_used < K (the
+    two-direction fallback) only the first K_used blocks get gradients."""
+    torch.manual_seed(1)
+    m = mb.MultiDirectionalMambaBlock(d_model=16, d_state=4, num_directions=4, grid_shape=(2, 3))
+    blocks = list(m.mamba_blocks)
+    bufs = mb._direction_stacks(m, blocks)
+    used = blocks[:K_used]
+    outs = mb._DirectionParams.apply(len(bufs), *[b[:K_used] for b in bufs],
+                                     *[mb._param(b, n) for n in mb.STACKED_PARAMS for b in used])
+    ws = [torch.randn(o.shape, generator=torch.Generator().manual_seed(i)) for i, o in enumerate(outs)]
+    for o, buf in zip(outs, bufs):
+        assert o.data_ptr() == buf.data_ptr()
+    sum((o * w).sum() for o, w in zip(outs, ws)).backward()
+    for w, name in zip(ws, mb.STACKED_PARAMS):
+        for k, b in enumerate(blocks):
+            g = mb._param(b, name).grad
+            if k < K_used:
+                assert torch.equal(g, w[k]), (name, k)
+            else:
+                assert g is None, (name, k)
