@@ -293,12 +293,26 @@ class _MambaCoreFn(torch.autograd.Function):
         # x_proj: dbc = xc @ W_x^T; the scan's du joins through the GEMM's beta
         # (in place: du is this backward's own buffer, so no copy of it is made)
         dxc = du.baddbmm_(d_dbc, W_x)
-        dW_x = torch.bmm(d_dbc.transpose(1, 2), xc)
+        dW_x = _tn_split_rows(d_dbc, xc)
         # conv + SiLU: dx lands in the first half of dxz
         dconv_w, dconv_b = conv_silu_backward_into(xb, conv_w, conv_b, _bnkd(dxc, bsz, n),
                                                    dxz[..., :din], tok)
         dA_log = dA * A  # A = -exp(A_log)
         return dxz, dconv_w, dconv_b, dW_x, dW_dt, db_dt, dA_log, dDv, None, None, None
+
+
+def _tn_split_rows(a, b, splits=8):
+    """a^T @ b per direction for a (K, M, P) and b (K, M, Q) with a long row
+    reduction (M = B*N) and small outputs: the rows are split into ``splits``
+    chunks, one batched GEMM over K*splits computes the partial products and
+    they are summed in a fixed order (deterministic).  The split keeps enough
+    workgroups in flight to stream b from HBM."""
+    K, M, P = a.shape
+    if M % splits or M // splits < 256:
+        return torch.bmm(a.transpose(1, 2), b)
+    m = M // splits
+    part = torch.bmm(a.reshape(K * splits, m, P).transpose(1, 2), b.reshape(K * splits, m, -1))
+    return part.view(K, splits, P, -1).sum(1)
 
 
 def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
