@@ -252,9 +252,10 @@ class _MambaCoreFn(torch.autograd.Function):
         xb, z = xz[..., :din], xz[..., din:]
         xc = torch.empty(K, bsz * n, din, dtype=torch.float32, device=dev)
         conv_silu_forward_into(xb, conv_w, conv_b, _bnkd(xc, bsz, n), tok)       # :170-171
-        dbc = torch.bmm(xc, W_x.transpose(1, 2).contiguous())                      # :174
+        # float32 operands: the GEMMs take the weights' transposed views as they are
+        dbc = torch.bmm(xc, W_x.transpose(1, 2))                                   # :174
         dt = dbc[..., :R]
-        delta_raw = torch.bmm(dt, W_dt.transpose(1, 2).contiguous())               # :180
+        delta_raw = torch.bmm(dt, W_dt.transpose(1, 2))                            # :180
         A = -torch.exp(A_log)                                                      # :184
         bc = _bnkd(dbc, bsz, n)
         save = not detach
@@ -287,8 +288,9 @@ class _MambaCoreFn(torch.autograd.Function):
             bc[..., R + ns:], Dv, z, y_raw, ckpt, dy, tok, ctx.chunk_len,
             du=_bnkd(du, bsz, n), ddelta_raw=_bnkd(ddelta_raw, bsz, n),
             dB=dbc_v[..., R:R + ns], dC=dbc_v[..., R + ns:], dz=dxz[..., din:])
-        # dt_proj: delta_raw = dt @ W_dt^T
-        d_dbc[..., :R] = torch.bmm(ddelta_raw, W_dt)
+        # dt_proj: delta_raw = dt @ W_dt^T; the GEMM writes the first R columns
+        # of d_dbc in place (row stride R + 2N is a valid leading dimension)
+        torch.bmm(ddelta_raw, W_dt, out=d_dbc[..., :R])
         dW_dt = torch.bmm(ddelta_raw.transpose(1, 2), dbc[..., :R])
         # x_proj: dbc = xc @ W_x^T; the scan's du joins through the GEMM's beta
         # (in place: du is this backward's own buffer, so no copy of it is made)
