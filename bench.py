@@ -25,6 +25,9 @@ peak of 8 TB/s.  traffic = HBM bytes per backward call at this shape from
 the rocprofv3 FETCH_SIZE and WRITE_SIZE counters, each scaled by what it
 reads for a 512 MiB copy (committed summary in profiles/, made with
 `bench.py --scan-driver`), or null when that summary is absent.
+valu_busy_per_simd: the share of that kernel's time its SIMDs' VALU is busy,
+from the SQ counters of the same summary (the backward is bound by VALU issue,
+so its HBM fraction follows from its instruction count).
 
 scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
 D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads,
@@ -184,15 +187,16 @@ def scan_driver(torch, scan, device):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")
 
 
-def measured_traffic(key):
-    """HBM bytes per call measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on
-    the scan at the VisionMamba step shape (a line `key: <bytes>` of the
-    committed profile summary), or None."""
+def measured_traffic(key, kind=int):
+    """A figure measured with rocprofv3 counters on the scan at the
+    VisionMamba step shape (a line `key: <value>` of the committed profile
+    summary: HBM bytes per call from FETCH_SIZE / WRITE_SIZE, or the
+    backward's VALU busy fraction from the SQ counters), or None."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
                 if line.startswith(key + ":"):
-                    return int(line.split(":", 1)[1].split()[0])
+                    return kind(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
     return None
@@ -308,6 +312,9 @@ def main():
         "launches": len(bwd),
         "fwd_call": {"achieved": round(fwd_b / fwd_t / 1e9, 1), "avg_launch_us": round(fwd_t * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(fwd_b)},
+        # the backward is VALU-issue bound: share of the kernel's time the
+        # SIMDs' VALU is busy (SQ counters, committed profile)
+        "valu_busy_per_simd": measured_traffic("bwd_valu_busy_per_simd", float),
     }
     scans = {
         "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 200, device),
