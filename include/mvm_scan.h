@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define MVM_ABI_VERSION 2
+#define MVM_ABI_VERSION 3
 
 /* status codes */
 #define MVM_OK 0
@@ -136,10 +136,10 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta,
  *                                             is delta_raw)
  *     y     = scan_fn(x, delta, A, B, C, D)  (:187)
  *     y     = y * silu(z)                    (:190)
- * plus their VJP.  softplus is applied inside the scan kernels as delta is
- * staged (forward and backward), and the gate as y is written back, so
- * neither makes its own pass over HBM; the gate's backward is one coalesced
- * pointwise pass ahead of the backward scan.  float32 only
+ * plus their VJP, and optionally A = -exp(A_log) (:184).  softplus is
+ * applied inside the scan kernels as delta is staged (forward and
+ * backward), the gate as y is written back and its gradient as dy is
+ * staged, so none of them makes its own pass over HBM.  float32 only
  * (in_dtype = out_dtype = MVM_F32).
  *
  * Layouts: `scan` gives the sizes, u / du strides (x_stride_*), the B-like
@@ -153,6 +153,11 @@ typedef struct mvm_scan_fused_desc {
   int64_t dt_stride_b, dt_stride_k, dt_stride_t;  /* delta_raw, ddelta_raw */
   int64_t y_stride_b, y_stride_k, y_stride_t;     /* y, y_raw, dy */
   int64_t z_stride_b, z_stride_k, z_stride_t;     /* z, dz */
+  /* Nonzero: the A argument holds A_log and the scan uses A = -exp(A_log)
+   * (mamba_block.py:184), formed in the kernels; the backward's dA output
+   * is then the gradient with respect to A_log (dA * A). */
+  int32_t a_is_log;
+  int32_t reserved; /* must be 0 */
 } mvm_scan_fused_desc;
 
 int mvm_scan_fused_validate(const mvm_scan_fused_desc* desc);

@@ -24,7 +24,7 @@ MVM_ERR_HIP = -4
 MVM_F32 = 0
 MVM_BF16 = 1
 MVM_MAX_DSTATE = 16
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -51,6 +51,7 @@ class FusedDesc(ctypes.Structure):
         ("dt_stride_b", _i64), ("dt_stride_k", _i64), ("dt_stride_t", _i64),
         ("y_stride_b", _i64), ("y_stride_k", _i64), ("y_stride_t", _i64),
         ("z_stride_b", _i64), ("z_stride_k", _i64), ("z_stride_t", _i64),
+        ("a_is_log", _i32), ("reserved", _i32),
     ]
 
 

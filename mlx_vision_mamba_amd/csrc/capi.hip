@@ -112,6 +112,7 @@ mvm::Geom make_geom(const mvm_scan_desc* d) {
   g.nchunk = d->seqlen > 0 ? ceil_div(d->seqlen, g.chunk_len) : 0;
   g.nck = ceil_div(d->seqlen, mvm::kCk);
   g.ncblk = ceil_div(d->dim, mvm::kChPerBlock);
+  g.a_log = 0;
   return g;
 }
 
@@ -312,6 +313,7 @@ int check_fused(const mvm_scan_fused_desc* fd) {
     return fail(MVM_ERR_INVALID_ARG, "fused row stride overlaps channels (dim=%lld)", (long long)dim);
   if (fd->scan.batch * fd->scan.ndir * fd->scan.seqlen > INT32_MAX)
     return fail(MVM_ERR_UNSUPPORTED, "batch*ndir*seqlen exceeds 2^31-1");
+  if (fd->reserved != 0) return fail(MVM_ERR_INVALID_ARG, "fused desc: reserved must be 0");
   return MVM_OK;
 }
 
@@ -320,6 +322,7 @@ mvm::Geom fused_geom(const mvm_scan_fused_desc* fd) {
   g.dsb = fd->dt_stride_b; g.dsk = fd->dt_stride_k; g.dst = fd->dt_stride_t;
   g.ysb = fd->y_stride_b;  g.ysk = fd->y_stride_k;  g.yst = fd->y_stride_t;
   g.zsb = fd->z_stride_b;  g.zsk = fd->z_stride_k;  g.zst = fd->z_stride_t;
+  g.a_log = fd->a_is_log != 0 ? 1 : 0;
   return g;
 }
 

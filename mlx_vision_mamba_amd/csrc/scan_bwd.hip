@@ -100,7 +100,7 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < gm.N) ? bf.A[(k * gm.D + d) * gm.N + n] * kLog2e : 0.f;
+    a2[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
     mu[j] = 0.f;
   }
   float dsum = 0.f;
@@ -165,7 +165,7 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
   const int64_t d = (idx / kStatePad) % gm.D;
   const int64_t bk = idx / (kStatePad * gm.D);
   const int64_t k = bk % gm.K;
-  const float a2 = n < gm.N ? bf.A[(k * gm.D + d) * gm.N + n] * kLog2e : 0.f;
+  const float a2 = n < gm.N ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
   float carry = 0.f;
   for (int64_t c = gm.nchunk - 1; c >= 0; --c) {
     const int64_t slot = (bk * gm.nchunk + c) * gm.D + d;
@@ -232,7 +232,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    an[j] = (dvalid && n < gm.N) ? bf.A[(k * gm.D + d) * gm.N + n] : 0.f;
+    an[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) : 0.f;
     a2[j] = an[j] * kLog2e;
     mu[j] = 0.f;
     dacc[j] = 0.0;
@@ -555,9 +555,14 @@ __device__ __forceinline__ void reduce_ad_part(const Geom& gm, const BwdBufs& bf
   sq[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && valid) {
-    const float t = static_cast<float>((sq[0][lane] + sq[1][lane]) + (sq[2][lane] + sq[3][lane]));
-    if (kind == 0)
-      bf.dA[(k * gm.D + d) * gm.N + n] = t;
+    const double sum = (sq[0][lane] + sq[1][lane]) + (sq[2][lane] + sq[3][lane]);
+    const float t = static_cast<float>(sum);
+    if (kind == 0) {
+      // with the A_log parametrisation, dA_log = dA * A (A = -exp(A_log))
+      const int64_t ia = (k * gm.D + d) * gm.N + n;
+      bf.dA[ia] = gm.a_log ? static_cast<float>(sum * static_cast<double>(load_A(bf.A, ia, 1)))
+                           : t;
+    }
     else
       (kind == 1 ? bf.dD : bf.ddbias)[k * gm.D + d] = t;
   }

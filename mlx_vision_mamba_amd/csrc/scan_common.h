@@ -104,6 +104,14 @@ __device__ __forceinline__ float softplus_grad_from_value(float sp) {
   return sp < 0.015625f ? series : direct;
 }
 
+// A of one (direction, channel, state): the array holds A itself, or A_log
+// with A = -exp(A_log) (mamba_block.py:184) when a_log is set.  Read once
+// per (d, n) by each block, so the accurate expf costs nothing measurable.
+__device__ __forceinline__ float load_A(const float* A, int64_t i, int a_log) {
+  const float v = A[i];
+  return a_log ? -expf(v) : v;
+}
+
 // 2^x on the transcendental unit (v_exp_f32); callers pre-scale by log2(e).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

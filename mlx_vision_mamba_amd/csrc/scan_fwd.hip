@@ -92,7 +92,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < gm.N) ? bf.A[(k * gm.D + d) * gm.N + n] * kLog2e : 0.f;
+    a2[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
     h[j] = 0.f;
   }
   const float dskip = (MODE == kMain && dvalid) ? bf.Dv[k * gm.D + d] : 0.f;
@@ -250,7 +250,7 @@ scan_fwd_carry_kernel(Geom gm, FwdBufs bf) {
   const int64_t d = (idx / kStatePad) % gm.D;
   const int64_t bk = idx / (kStatePad * gm.D);
   const int64_t k = bk % gm.K;
-  const float a2 = n < gm.N ? bf.A[(k * gm.D + d) * gm.N + n] * kLog2e : 0.f;
+  const float a2 = n < gm.N ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
   float carry = 0.f;
   for (int64_t c = 0; c < gm.nchunk; ++c) {
     const int64_t slot = (bk * gm.nchunk + c) * gm.D + d;

@@ -20,6 +20,7 @@ struct Geom {
   int64_t nchunk;          // ceil(L / chunk_len)
   int64_t nck;             // ceil(L / kCk), checkpoint slots per (b, k, d)
   int64_t ncblk;           // ceil(D / 64), channel blocks
+  int32_t a_log;           // 1: the A array holds A_log, A = -exp(A_log)
 };
 
 struct FwdBufs {

@@ -25,9 +25,10 @@ Activations between the projections are kept direction-major,
 copies.
 
 The direction blocks' per-direction parameters (in_proj, conv1d, x_proj,
-dt_proj, A_log, D) are slices of one (K, ...) buffer per kind owned by the
-direction module, so the batched operands are views, not per-step
-concatenations; each buffer's gradient returns to the K parameters as its K
+dt_proj, A_log, D, out_proj) are slices of one (K, ...) buffer per kind owned
+by the direction module, so the batched operands are views, not per-step
+concatenations (out_proj's (E, K*D_inner) operand is one reordering copy);
+each buffer's gradient returns to the K parameters as its K
 slices.  The buffers are (re)built at the first forward and whenever a
 parameter stops being its slice (after ``.to()``, or a replaced parameter).
 """
@@ -165,7 +166,7 @@ class MultiDirectionalMambaBlock(nn.Module):
 
 # per-direction parameters stored as slices of one (K, ...) buffer per kind
 STACKED_PARAMS = ("in_proj.weight", "conv1d.weight", "conv1d.bias", "x_proj.weight",
-                  "dt_proj.weight", "dt_proj.bias", "A_log", "D")
+                  "dt_proj.weight", "dt_proj.bias", "A_log", "D", "out_proj.weight")
 
 
 def _param(blk, path):
@@ -203,7 +204,9 @@ def _direction_stacks(owner, blocks):
 class _DirectionParams(torch.autograd.Function):
     """(buffers..., parameters...) -> the buffers, differentiable w.r.t. the
     parameters that are their slices: the backward hands each buffer's
-    gradient to its K parameters as K contiguous slices (no copy)."""
+    gradient to its K parameters as K contiguous slices (a gradient that
+    arrives strided, as out_proj's does, is made contiguous once, so the
+    parameters take their slices without a copy each)."""
 
     @staticmethod
     def forward(ctx, nbuf, *tensors):
@@ -215,7 +218,7 @@ class _DirectionParams(torch.autograd.Function):
     def backward(ctx, *grads):
         out = [None] * (1 + ctx.nbuf)
         for g in grads:
-            out += list(g.unbind(0)) if g is not None else [None] * ctx.K
+            out += list(g.contiguous().unbind(0)) if g is not None else [None] * ctx.K
         return tuple(out)
 
 
@@ -240,6 +243,8 @@ class _MambaCoreFn(torch.autograd.Function):
       dbc   = x_proj(xc)                                   (K, B*N, R + 2N)
       delta = softplus(dt_proj(dbc[:R]) + dt_bias)         inside the scan
       y     = scan(xc, delta, -exp(A_log), B, C, D) * silu(z)
+    The scan kernels take A_log and form A = -exp(A_log) themselves; their
+    dA output is the gradient of A_log.
     """
 
     @staticmethod
@@ -256,26 +261,25 @@ class _MambaCoreFn(torch.autograd.Function):
         dbc = torch.bmm(xc, W_x.transpose(1, 2))                                   # :174
         dt = dbc[..., :R]
         delta_raw = torch.bmm(dt, W_dt.transpose(1, 2))                            # :180
-        A = -torch.exp(A_log)                                                      # :184
         bc = _bnkd(dbc, bsz, n)
         save = not detach
-        y, y_raw, ckpt = scan_fused_forward(_bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A,
+        y, y_raw, ckpt = scan_fused_forward(_bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A_log,
                                             bc[..., R:R + ns], bc[..., R + ns:], Dv, z, tok,
-                                            chunk_len, save=save)                  # :181, :187, :190
+                                            chunk_len, save=save, a_is_log=True)   # :181-190
         if save:
-            ctx.save_for_backward(xz, conv_w, conv_b, W_x, W_dt, b_dt, A, Dv, tok, xc, dbc,
+            ctx.save_for_backward(xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, tok, xc, dbc,
                                   delta_raw, y_raw, ckpt)
             ctx.chunk_len = chunk_len
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        (xz, conv_w, conv_b, W_x, W_dt, b_dt, A, Dv, tok, xc, dbc, delta_raw, y_raw,
+        (xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, tok, xc, dbc, delta_raw, y_raw,
          ckpt) = ctx.saved_tensors
         bsz, n, K, d2 = xz.shape
         din = d2 // 2
         R = W_dt.shape[2]
-        ns = A.shape[2]
+        ns = A_log.shape[2]
         dev = xz.device
         xb, z = xz[..., :din], xz[..., din:]
         dxz = torch.empty(xz.shape, dtype=torch.float32, device=dev)
@@ -283,11 +287,11 @@ class _MambaCoreFn(torch.autograd.Function):
         du = torch.empty_like(xc)
         ddelta_raw = torch.empty_like(delta_raw)
         bc, dbc_v = _bnkd(dbc, bsz, n), _bnkd(d_dbc, bsz, n)
-        _, _, db_dt, dA, _, _, dDv, _ = scan_fused_backward(
-            _bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A, bc[..., R:R + ns],
+        _, _, db_dt, dA_log, _, _, dDv, _ = scan_fused_backward(
+            _bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A_log, bc[..., R:R + ns],
             bc[..., R + ns:], Dv, z, y_raw, ckpt, dy, tok, ctx.chunk_len,
             du=_bnkd(du, bsz, n), ddelta_raw=_bnkd(ddelta_raw, bsz, n),
-            dB=dbc_v[..., R:R + ns], dC=dbc_v[..., R + ns:], dz=dxz[..., din:])
+            dB=dbc_v[..., R:R + ns], dC=dbc_v[..., R + ns:], dz=dxz[..., din:], a_is_log=True)
         # dt_proj: delta_raw = dt @ W_dt^T; the GEMM writes the first R columns
         # of d_dbc in place (row stride R + 2N is a valid leading dimension)
         torch.bmm(ddelta_raw, W_dt, out=d_dbc[..., :R])
@@ -299,7 +303,6 @@ class _MambaCoreFn(torch.autograd.Function):
         # conv + SiLU: dx lands in the first half of dxz
         dconv_w, dconv_b = conv_silu_backward_into(xb, conv_w, conv_b, _bnkd(dxc, bsz, n),
                                                    dxz[..., :din], tok)
-        dA_log = dA * A  # A = -exp(A_log)
         return dxz, dconv_w, dconv_b, dW_x, dW_dt, db_dt, dA_log, dDv, None, None, None
 
 
@@ -332,7 +335,7 @@ def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
         per = _DirectionParams.apply(len(stacks), *[buf[:K] for buf in stacks],
                                      *[_param(b, name) for name in STACKED_PARAMS
                                        for b in blocks])
-    W_in, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv = per
+    W_in, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, W_out = per
     W_in = W_in.reshape(K * 2 * din, W_in.shape[-1])                          # (K*2D, E)
     xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165-167
     conv_w = conv_w.reshape(K, din, b0.d_conv)                                 # (K, Din, d_conv)
@@ -345,5 +348,7 @@ def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
     if detach:
         args = [t.detach() for t in args]
     y = _MambaCoreFn.apply(*args, tok, mode_chunk_len(scan_mode), detach)     # :170-190
-    W_out = torch.cat([blk.out_proj.weight for blk in blocks], 1) if K > 1 else b0.out_proj.weight
+    # (K, E, Din) -> (E, K*Din): the out_proj of the concatenated directions
+    # is their (atomic-free) sum
+    W_out = W_out.permute(1, 0, 2).reshape(W_out.shape[1], K * din)
     return F.linear(y.reshape(bsz, n, K * din), W_out)                         # :191, :562-566

@@ -234,8 +234,9 @@ def _no_overlap(t):
     return True
 
 
-def _fused_desc(u, delta_raw, Bm, y, z, tok, chunk_len):
+def _fused_desc(u, delta_raw, Bm, y, z, tok, chunk_len, a_is_log=False):
     fd = _lib.FusedDesc()
+    fd.a_is_log = int(bool(a_is_log))
     fd.scan = _make_desc(u, Bm, torch.float32, torch.float32, tok, chunk_len)
     fd.dt_stride_b, fd.dt_stride_t, fd.dt_stride_k = _bkd(delta_raw)
     fd.y_stride_b, fd.y_stride_t, fd.y_stride_k = _bkd(y)
@@ -266,9 +267,10 @@ def _check_fused(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z):
 
 
 def scan_fused_forward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, tok=None, chunk_len=0,
-                       save=False):
+                       save=False, a_is_log=False):
     """y = scan(u, softplus(delta_raw + delta_bias), A, B, C, D) * silu(z)
-    (mamba_block.py:180-190) in one launch sequence.
+    (mamba_block.py:180-190) in one launch sequence.  With ``a_is_log`` the
+    A argument holds A_log and the kernels use A = -exp(A_log) (:184).
 
     u, delta_raw, z: (B, L, K, D) float32 views with channel stride 1 and any
     other strides (z may be None: no gate); delta_bias (K, D) or None;
@@ -280,7 +282,7 @@ def scan_fused_forward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, tok=None, chu
     dev = u.device
     L = u.shape[1]
     y = torch.empty(u.shape, dtype=torch.float32, device=dev)
-    fd = _fused_desc(u, delta_raw, Bm, y, z, tok, _resolve_chunk(L, chunk_len))
+    fd = _fused_desc(u, delta_raw, Bm, y, z, tok, _resolve_chunk(L, chunk_len), a_is_log)
     lib = _lib.lib()
     with torch.cuda.device(dev):
         y_raw = torch.empty_like(y) if (save and z is not None) else None
@@ -307,8 +309,11 @@ def scan_fused_forward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, tok=None, chu
 
 
 def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt, dy, tok=None,
-                        chunk_len=0, du=None, ddelta_raw=None, dB=None, dC=None, dz=None):
-    """VJP of scan_fused_forward for dy (gradient of the gated y).
+                        chunk_len=0, du=None, ddelta_raw=None, dB=None, dC=None, dz=None,
+                        a_is_log=False):
+    """VJP of scan_fused_forward for dy (gradient of the gated y).  With
+    ``a_is_log`` (A holds A_log) the returned dA is the gradient with
+    respect to A_log.
 
     Output views may be passed in (any strides with channel stride 1, e.g.
     slices of a larger gradient buffer); missing ones are allocated with
@@ -349,7 +354,7 @@ def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt,
     ddelta_bias = torch.empty_like(delta_bias) if delta_bias is not None else None
     dA = torch.empty(A.shape, dtype=torch.float32, device=dev)
     dD = torch.empty(Dv.shape, dtype=torch.float32, device=dev)
-    fd = _fused_desc(u, delta_raw, Bm, dy, z, tok, _resolve_chunk(L, chunk_len))
+    fd = _fused_desc(u, delta_raw, Bm, dy, z, tok, _resolve_chunk(L, chunk_len), a_is_log)
     lib = _lib.lib()
     with torch.cuda.device(dev):
         nbytes = _lib.check(lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, int(z is not None)))

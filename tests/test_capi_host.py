@@ -214,6 +214,20 @@ def test_fused_bad_descriptors_rejected(field, value, code):
     assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == code
 
 
+def test_fused_a_log_flag_and_reserved_field():
+    """a_is_log selects the A_log parametrisation (any value accepted, same
+    workspace); the reserved field must stay 0."""
+    lib = _lib.lib()
+    fd = _fdesc()
+    base = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1)
+    fd.a_is_log = 1
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == 0
+    assert lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1) == base
+    fd.reserved = 7
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == _lib.MVM_ERR_INVALID_ARG
+    assert "reserved" in _lib.last_error()
+
+
 def test_fused_is_float32_only():
     lib = _lib.lib()
     fd = _fdesc()

@@ -49,7 +49,7 @@ def _bnkd(t, bsz, L):
     return t.view(K, bsz, L, X).permute(1, 2, 0, 3)
 
 
-def _run_gpu(c, dev, chunk_len=0):
+def _run_gpu(c, dev, chunk_len=0, a_is_log=False):
     from mlx_vision_mamba_amd import scan
     K, bsz, L, D = c["u"].shape
     R, N = c["R"], c["N"]
@@ -60,21 +60,24 @@ def _run_gpu(c, dev, chunk_len=0):
     z = xz[..., D:] if c["gate"] else None
     b = c["b"].to(dev) if c["b"] is not None else None
     A, Dv = c["A"].to(dev), c["Dv"].to(dev)
+    if a_is_log:
+        A = torch.log(-A)  # the kernels form A = -exp(A_log)
     tok = torch.tensor(c["tok"], device=dev)
     bc = _bnkd(dbc, bsz, L)
     args = (_bnkd(u, bsz, L), _bnkd(draw, bsz, L), b, A, bc[..., R:R + N], bc[..., R + N:], Dv, z)
-    y, y_raw, ck = scan.scan_fused_forward(*args, tok=tok, chunk_len=chunk_len, save=True)
+    y, y_raw, ck = scan.scan_fused_forward(*args, tok=tok, chunk_len=chunk_len, save=True,
+                                           a_is_log=a_is_log)
     dxz = torch.full_like(xz, float("nan"))
     d_dbc = torch.full_like(dbc, float("nan"))
     dd_v = _bnkd(d_dbc, bsz, L)
     out = scan.scan_fused_backward(*args, y_raw, ck, c["g"].to(dev), tok=tok, chunk_len=chunk_len,
                                    dB=dd_v[..., R:R + N], dC=dd_v[..., R + N:],
-                                   dz=dxz[..., D:] if c["gate"] else None)
+                                   dz=dxz[..., D:] if c["gate"] else None, a_is_log=a_is_log)
     torch.cuda.synchronize()
     return y, out, d_dbc, dxz
 
 
-def _check(c, y, out, d_dbc, dxz):
+def _check(c, y, out, d_dbc, dxz, a_is_log=False):
     K, bsz, L, D = c["u"].shape
     R, N = c["R"], c["N"]
     du, ddr, db, dA, dB, dC, dD, dz = out
@@ -98,7 +101,8 @@ def _check(c, y, out, d_dbc, dxz):
         assert_close(y[:, idx, k], y_ref, f"y[k={k}]")
         assert_close(du[:, idx, k], r[0], f"du[k={k}]")
         assert_close(ddr[:, idx, k], r[1], f"ddelta_raw[k={k}]", scale=scale)
-        assert_close(dA[k], r[3], f"dA[k={k}]")
+        # with A_log the kernels return dA_log = dA * A (chain rule of A = -exp(A_log))
+        assert_close(dA[k], r[3] * Ak if a_is_log else r[3], f"dA[k={k}]")
         assert_close(dB[:, idx, k], r[4], f"dB[k={k}]")
         assert_close(dC[:, idx, k], r[5], f"dC[k={k}]")
         assert_close(dD[k], r[6], f"dD[k={k}]")
@@ -135,6 +139,17 @@ def test_fused_chunked_long_sequence(cuda):
     print("case: fused chunked L=700 chunk=64", flush=True)
     c = _case(1, 700, 2, 64, 16, 4, seed=5)
     _check(c, *_run_gpu(c, cuda, chunk_len=64))
+
+
+@pytest.mark.parametrize("chunk_len", [0, 64, 32])
+def test_fused_a_log_parametrisation(cuda, chunk_len):
+    """A passed as A_log (A = -exp(A_log) formed in the kernels): y and every
+    gradient match the oracle, dA becoming dA * A, with one time chunk and
+    with the two-pass carry (whose aggregate passes read A too): 5 chunks
+    fold their carry in the main pass, 10 use the separate carry kernels."""
+    print(f"case: fused A_log chunk_len={chunk_len}", flush=True)
+    c = _case(1, 300, 4, 64, 16, 6, seed=9, grid=(15, 20))
+    _check(c, *_run_gpu(c, cuda, chunk_len=chunk_len, a_is_log=True), a_is_log=True)
 
 
 def test_fused_equals_unfused_composition(cuda):
