@@ -85,6 +85,7 @@ def bench_step(torch, mvm, scan, steps, warmup, device):
     t0 = time.perf_counter()
     for _ in range(steps):
         loss = step()
+    enqueued = time.perf_counter() - t0  # host time to issue the K steps
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     scan.set_scan_timing(None)
@@ -93,7 +94,7 @@ def bench_step(torch, mvm, scan, steps, warmup, device):
     per = {"fwd": [], "bwd": []}
     for kind, e0, e1, nbytes in records:
         per[kind].append((e0.elapsed_time(e1) * 1e-3, nbytes))
-    return elapsed, per
+    return elapsed, per, enqueued
 
 
 def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
@@ -293,7 +294,7 @@ def main():
         print(json.dumps({"tuned_gemms": args.tune_gemms}), flush=True)
         return
     tuned = False if args.default_gemms else gemm_tuning.load()
-    elapsed, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
+    elapsed, per, enqueued = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
     imgs = 32 * args.steps / elapsed
 
     bwd = per["bwd"]
@@ -324,6 +325,9 @@ def main():
         "metric": METRIC, "value": round(imgs, 2), "unit": "imgs/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        # host time to issue one step (python, autograd, launches): the step
+        # is host-bound when this approaches ms_per_step
+        "host_issue_ms_per_step": round(enqueued / args.steps * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded N(0,1) images, random-init weights)",
         "config": {"workload": "VisionMamba-2D K=4 train step (fwd + mean loss + bwd + AdamW)",

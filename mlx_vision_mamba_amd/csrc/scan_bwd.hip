@@ -114,6 +114,10 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
     pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
   };
   auto store_tile = [&](int buf) {
+    mask_xtile(pd, cok);
+    mask_xtile(pg, cok);
+    if (gate) mask_xtile(pz, cok);
+    pc = mask_stile(pc, gm.N, tid);
     stage_delta(pd);
     stage_g(pg);
     store_xtile(sD[buf], pd, tid);
@@ -415,6 +419,16 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     pck1 = load_ckpt(ts + kCk);
   };
   auto store_tile = [&](int buf, const TileRows& rows, int nt) {
+    // the prefetched values are first consumed here, after the tile's math
+    mask_xtile(pu, cok);
+    mask_xtile(pd, cok);
+    mask_xtile(pg, cok);
+    if (gate) {
+      mask_xtile(pz, cok);
+      mask_xtile(pyr, cok);
+    }
+    pb = mask_stile(pb, gm.N, tid);
+    pc = mask_stile(pc, gm.N, tid);
     stage_delta(pd);
     stage_gate(pg, rows, nt);
     store_xtile(sU[buf], pu, tid);

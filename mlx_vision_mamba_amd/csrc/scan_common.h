@@ -219,8 +219,10 @@ __device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int64_t ts, in
 
 // Channel-indexed tile rows: v[r] = p[base + rows.r[r] * st + lane] (base
 // includes the block's first channel).  Out-of-range channels (cok false)
-// read channel 0 of the row, always in bounds, and yield 0: no load waits
-// behind a divergent branch.
+// read channel 0 of the row, always in bounds, so no load waits behind a
+// divergent branch; their values are zeroed by mask_xtile when the tile is
+// staged.  Nothing here consumes the loaded values, so a prefetch issued
+// before a tile's math is not waited for until the next tile is staged.
 template <typename T>
 __device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ p, int64_t base,
                                            const TileRows& rows, int64_t st, int lch, bool cok) {
@@ -228,16 +230,20 @@ __device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ 
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const T* rowp = p + (base + static_cast<int64_t>(rows.r[r]) * st);  // SGPR pointer
-    const float x = to_f32(rowp[lc]);
-    v[r] = cok ? x : 0.f;
+    v[r] = to_f32(rowp[lc]);
   }
+}
+__device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = cok ? v[r] : 0.f;
 }
 
 // LDS row of the state-indexed value a thread stages (row w + 4 (l >> 4)).
 __device__ __forceinline__ int stile_row(int tid) { return (tid >> 6) + 4 * ((tid >> 4) & 3); }
 
 // State-indexed tile value of this thread: state tid & 15 of row
-// stile_row(tid); states >= N yield 0.
+// stile_row(tid); states >= N read state 0 and are zeroed by mask_stile
+// when the tile is staged.
 template <typename T>
 __device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base,
                                             const TileRows& rows, int64_t st, int64_t N, int tid) {
@@ -245,9 +251,10 @@ __device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t bas
   const int64_t o0 = static_cast<int64_t>(rows.r[0]) * st, o1 = static_cast<int64_t>(rows.r[1]) * st;
   const int64_t o2 = static_cast<int64_t>(rows.r[2]) * st, o3 = static_cast<int64_t>(rows.r[3]) * st;
   const int64_t off = q == 0 ? o0 : (q == 1 ? o1 : (q == 2 ? o2 : o3));
-  const bool nok = n < N;
-  const float x = ld(p, base + off + (nok ? n : 0));
-  return nok ? x : 0.f;
+  return ld(p, base + off + (n < N ? n : 0));
+}
+__device__ __forceinline__ float mask_stile(float x, int64_t N, int tid) {
+  return (tid & 15) < N ? x : 0.f;
 }
 
 __device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float (&v)[4], int tid) {

@@ -178,6 +178,14 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     pb = load_stile(Bm, bcbase, rows, gm.bst, gm.N, tid);
     if (MODE == kMain) pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
   };
+  // zero the out-of-range channels / states of a prefetched tile: the first
+  // use of its values, after the current tile's math
+  auto mask_tile = [&](float (&pu)[4], float (&pd)[4], float& pb, float& pc) {
+    mask_xtile(pu, cok);
+    mask_xtile(pd, cok);
+    pb = mask_stile(pb, gm.N, tid);
+    pc = mask_stile(pc, gm.N, tid);
+  };
   auto store_tile = [&](int buf, const float (&pu)[4], const float (&pd)[4], float pb, float pc) {
     store_xtile(sU[buf], pu, tid);
     store_xtile(sD[buf], pd, tid);
@@ -190,6 +198,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   TileRows rc = tile_rows<TOK>(tok, t0, gm.L, tid);  // rows of the tile being computed
   TileRows rp = rc;                                   // rows of the previous tile
   load_tile(rc, pu, pd, pb, pc);
+  mask_tile(pu, pd, pb, pc);
   stage_delta(pd);
   store_tile(0, pu, pd, pb, pc);
 
@@ -220,6 +229,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       }
     }
     if (more) {
+      mask_tile(pu, pd, pb, pc);
       stage_delta(pd);
       store_tile(buf ^ 1, pu, pd, pb, pc);
     }
