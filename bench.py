@@ -1,7 +1,7 @@
 """Benchmark: VisionMamba-2D K=4 train step on one MI355X, plus the selective
 scan's fwd+VJP bandwidth, printed as one JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--eager]
     python bench.py --scan-driver     (profiling driver, see scan_driver)
 
 Workload (the step timed): VisionMamba encoder, 2D, K=4 scan directions,
@@ -14,12 +14,18 @@ GEMMs use the TunableOp picks recorded for this step on MI355X
 (mlx_vision_mamba_amd/tuning/, read-only; --default-gemms for the library
 defaults).  Inputs are resident on the GPU before the
 timed region; W untimed warm-up steps, then exactly K steps between two
-device synchronisations.  value = images / second.
+device synchronisations.  value = images / second.  The step is captured once
+in a HIP graph (after the warm-up) and the K timed steps are K replays of it,
+so the host issues one launch per step instead of ~190 kernels through
+Python and autograd (whose ~7-10 ms per step otherwise approaches the GPU
+time on slower hosts); --eager times the eager loop instead.
 
 roofline: the fused scan backward call (the block's scan VJP with the
 softplus and silu-gate gradients inside it; the largest hand-written piece
 of the step; its kernels are listed in "kernel"), timed with HIP events on
-the stream it runs on for every launch inside the timed region; achieved =
+the stream it runs on, for every launch of an eager timed region of K steps
+(after the graph replays; HIP events cannot be timed inside a captured graph
+on ROCm, and the replayed kernels are the same); achieved =
 algorithmic bytes per launch / mean launch time, against the MI355X HBM3E
 peak of 8 TB/s.  traffic = HBM bytes per backward call at this shape from
 the rocprofv3 FETCH_SIZE and WRITE_SIZE counters, each scaled by what it
@@ -64,37 +70,86 @@ def _seeded_model(torch, mvm, device):
     return model.to(device)
 
 
-def bench_step(torch, mvm, scan, steps, warmup, device):
+def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
+    """Time `steps` train steps after `warmup` untimed ones.
+
+    graph=True: the step (forward, loss, backward, AdamW) is captured once in
+    a HIP graph and the timed region is `steps` replays of it.  ROCm cannot
+    time events inside a captured graph, so a second timed region follows:
+    `steps` eager steps of the same model, with a HIP event pair around
+    every scan launch (the launch records).  graph=False: the eager region
+    only.  Returns {"elapsed", "issued"} of the value region, the eager
+    region's {"elapsed", "issued"} and the launch records."""
     model = _seeded_model(torch, mvm, device)
     gen = torch.Generator().manual_seed(1)
     x = torch.randn(32, 224, 224, 1, generator=gen).to(device)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    # the captured step needs a capturable optimizer (its step count lives on
+    # the device); the eager region uses the plain fused AdamW, whose host
+    # path is the cheaper one
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=graph)
+    opt_eager = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True) if graph else opt
 
-    def step():
-        opt.zero_grad(set_to_none=True)
+    def step(o=opt):
+        o.zero_grad(set_to_none=True)
         loss = model(x).mean()
         loss.backward()
-        opt.step()
+        o.step()
         return loss
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    records = []
-    scan.set_scan_timing(records)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        loss = step()
-    enqueued = time.perf_counter() - t0  # host time to issue the K steps
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    scan.set_scan_timing(None)
-    if not math.isfinite(float(loss)):
-        raise RuntimeError("non-finite loss")
+    def eager_region():
+        records = []
+        for _ in range(3 if graph else 0):  # the eager optimizer's first steps
+            step(opt_eager)
+        torch.cuda.synchronize()
+        scan.set_scan_timing(records)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step(opt_eager)
+        issued = time.perf_counter() - t0  # host time to issue the K steps
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        scan.set_scan_timing(None)
+        if not math.isfinite(float(loss.detach())):
+            raise RuntimeError("non-finite loss")
+        return {"elapsed": elapsed, "issued": issued}, records
+
+    if not graph:
+        for _ in range(warmup):
+            step()
+        region, records = eager_region()
+        value_region = region
+    else:
+        # warm-up on a side stream (as capture requires); the first forward
+        # also lays the direction parameters out in their stacked buffers
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(max(warmup, 3)):
+                step()
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize()
+        opt.zero_grad(set_to_none=True)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            gloss = model(x).mean()
+            gloss.backward()
+            opt.step()
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        issued = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        if not math.isfinite(float(gloss.detach())):
+            raise RuntimeError("non-finite loss")
+        value_region = {"elapsed": elapsed, "issued": issued}
+        region, records = eager_region()
     per = {"fwd": [], "bwd": []}
     for kind, e0, e1, nbytes in records:
         per[kind].append((e0.elapsed_time(e1) * 1e-3, nbytes))
-    return elapsed, per, enqueued
+    return value_region, region, per
 
 
 def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
@@ -264,6 +319,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time the eager step loop instead of replays of the captured HIP graph")
     ap.add_argument("--tune-gemms", metavar="CSV", default=None,
                     help="tune the step's GEMMs with TunableOp (2 steps) and write the picks to CSV")
     ap.add_argument("--default-gemms", action="store_true",
@@ -290,11 +347,13 @@ def main():
         return
     if args.tune_gemms:
         gemm_tuning.start_tuning(args.tune_gemms)
-        bench_step(torch, mvm, scan, 2, 1, device)
+        bench_step(torch, mvm, scan, 2, 1, device, graph=False)
         print(json.dumps({"tuned_gemms": args.tune_gemms}), flush=True)
         return
     tuned = False if args.default_gemms else gemm_tuning.load()
-    elapsed, per, enqueued = bench_step(torch, mvm, scan, args.steps, args.warmup, device)
+    value_region, eager, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device,
+                                          graph=not args.eager)
+    elapsed, enqueued = value_region["elapsed"], value_region["issued"]
     imgs = 32 * args.steps / elapsed
 
     bwd = per["bwd"]
@@ -328,6 +387,9 @@ def main():
         # host time to issue one step (python, autograd, launches): the step
         # is host-bound when this approaches ms_per_step
         "host_issue_ms_per_step": round(enqueued / args.steps * 1e3, 3),
+        "execution": "eager" if args.eager else "HIP graph replay of the captured step",
+        "eager_ms_per_step": round(eager["elapsed"] / args.steps * 1e3, 3),
+        "eager_host_issue_ms_per_step": round(eager["issued"] / args.steps * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded N(0,1) images, random-init weights)",
         "config": {"workload": "VisionMamba-2D K=4 train step (fwd + mean loss + bwd + AdamW)",

@@ -186,3 +186,49 @@ def test_stacked_parameters_follow_optimizer_and_moves(cuda):
     _train_steps(fresh, x, 2)
     for (n, p), (_, q) in zip(model.named_parameters(), fresh.named_parameters()):
         assert torch.allclose(p, q, rtol=1e-4, atol=1e-6), n
+
+
+def test_graph_captured_step_matches_eager(cuda):
+    """The whole train step (forward, loss, backward, fused AdamW) captured
+    in a HIP graph: each replay, with eager steps of a twin model and
+    synchronisations between the replays, gives the twin's loss and
+    parameters."""
+    kw = dict(img_size=32, patch_size=8, embed_dim=32, depth=2, input_dim=2)
+
+    def make():
+        torch.manual_seed(9)
+        m = mvm.VisionMamba(**kw).to(cuda)
+        return m, torch.optim.AdamW(m.parameters(), lr=1e-2, fused=True, capturable=True)
+
+    x = torch.randn(4, 32, 32, 1, generator=torch.Generator().manual_seed(10)).to(cuda)
+    (mg, og), (me, oe) = make(), make()
+
+    def step(m, o):
+        o.zero_grad(set_to_none=True)
+        loss = m(x).square().mean()
+        loss.backward()
+        o.step()
+        return loss
+
+    side = torch.cuda.Stream(cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step(mg, og)
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    for _ in range(3):
+        step(me, oe)
+    torch.cuda.synchronize()
+    og.zero_grad(set_to_none=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gloss = mg(x).square().mean()
+        gloss.backward()
+        og.step()
+    for i in range(5):
+        g.replay()
+        eloss = step(me, oe)
+        torch.cuda.synchronize()
+        assert torch.allclose(gloss.detach(), eloss.detach(), rtol=1e-6, atol=0), i
+        for (n, p), (_, q) in zip(mg.named_parameters(), me.named_parameters()):
+            assert torch.allclose(p, q, rtol=1e-5, atol=1e-7), (i, n)
