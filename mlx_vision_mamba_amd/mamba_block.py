@@ -169,11 +169,29 @@ STACKED_PARAMS = ("in_proj.weight", "conv1d.weight", "conv1d.bias", "x_proj.weig
                   "dt_proj.weight", "dt_proj.bias", "A_log", "D", "out_proj.weight")
 
 
+_STACKED_PATHS = tuple((tuple(n.split(".")[:-1]), n.split(".")[-1]) for n in STACKED_PARAMS)
+
+
 def _param(blk, path):
-    obj = blk
-    for part in path.split("."):
-        obj = getattr(obj, part)
-    return obj
+    """The parameter at dotted ``path`` of ``blk``, by direct registry lookups
+    (the same objects attribute access returns, without Module.__getattr__)."""
+    *mods, name = path.split(".")
+    for m in mods:
+        blk = blk._modules[m]
+    return blk._parameters[name]
+
+
+def _params_of(blocks):
+    """STACKED_PARAMS of each block, kind-major: [[kind 0 of block 0, ...], ...]."""
+    out = []
+    for mods, name in _STACKED_PATHS:
+        row = []
+        for b in blocks:
+            for m in mods:
+                b = b._modules[m]
+            row.append(b._parameters[name])
+        out.append(row)
+    return out
 
 
 def _is_slice_of(p, buf, k):
@@ -186,18 +204,26 @@ def _direction_stacks(owner, blocks):
     """The (K, ...) buffers whose k-th slices are the parameters of blocks[k],
     one per name of STACKED_PARAMS, kept on ``owner``.  Rebuilt (values
     copied from the current parameters, which then become slices of the new
-    buffers) when any parameter is not its slice."""
-    params = [[_param(b, name) for b in blocks] for name in STACKED_PARAMS]
-    bufs = owner.__dict__.get("_param_stacks")
-    if bufs is not None and all(_is_slice_of(p, buf, k) for buf, ps in zip(bufs, params)
-                                for k, p in enumerate(ps)):
-        return bufs
+    buffers) when any parameter is not its slice.  The per-call check
+    compares each parameter's data pointer, shape and dtype with those its
+    slice was given (the buffers are held here, so their memory is never
+    reused while the pointers are compared)."""
+    params = _params_of(blocks)
+    cache = owner.__dict__.get("_param_stacks")
+    if cache is not None:
+        bufs, expect = cache
+        flat = [p for ps in params for p in ps]
+        if len(flat) == len(expect) and all(
+                p.data_ptr() == ptr and p.dtype is dt and p.shape == shp
+                for p, (ptr, dt, shp) in zip(flat, expect)):
+            return bufs
     with torch.no_grad():
         bufs = [torch.stack([p.detach() for p in ps], 0) for ps in params]
         for buf, ps in zip(bufs, params):
             for k, p in enumerate(ps):
                 p.data = buf[k]
-    owner.__dict__["_param_stacks"] = bufs
+    expect = [(p.data_ptr(), p.dtype, p.shape) for ps in params for p in ps]
+    owner.__dict__["_param_stacks"] = (bufs, expect)
     return bufs
 
 
@@ -330,11 +356,10 @@ def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
     bsz, n, _ = h.shape
     din, ns, R = b0.d_inner, b0.d_state, b0.dt_rank
     if stacks is None:
-        per = [_param(b0, name).unsqueeze(0) for name in STACKED_PARAMS]
+        per = [ps[0].unsqueeze(0) for ps in _params_of([b0])]
     else:
         per = _DirectionParams.apply(len(stacks), *[buf[:K] for buf in stacks],
-                                     *[_param(b, name) for name in STACKED_PARAMS
-                                       for b in blocks])
+                                     *[p for ps in _params_of(blocks) for p in ps])
     W_in, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, W_out = per
     W_in = W_in.reshape(K * 2 * din, W_in.shape[-1])                          # (K*2D, E)
     xz = F.linear(h, W_in).view(bsz, n, K, 2 * din)                            # :165-167
