@@ -77,9 +77,10 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     a HIP graph and the timed region is `steps` replays of it.  ROCm cannot
     time events inside a captured graph, so a second timed region follows:
     `steps` eager steps of the same model, with a HIP event pair around
-    every scan launch (the launch records).  graph=False: the eager region
-    only.  Returns {"elapsed", "issued"} of the value region, the eager
-    region's {"elapsed", "issued"} and the launch records."""
+    every scan launch (the launch records).  graph=False, or a capture that
+    the runtime refuses: the eager region only.  Returns {"elapsed",
+    "issued"} of the value region, the eager region's {"elapsed", "issued"},
+    the launch records and the mode that was timed."""
     model = _seeded_model(torch, mvm, device)
     gen = torch.Generator().manual_seed(1)
     x = torch.randn(32, 224, 224, 1, generator=gen).to(device)
@@ -113,12 +114,7 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
             raise RuntimeError("non-finite loss")
         return {"elapsed": elapsed, "issued": issued}, records
 
-    if not graph:
-        for _ in range(warmup):
-            step()
-        region, records = eager_region()
-        value_region = region
-    else:
+    def graph_region():
         # warm-up on a side stream (as capture requires); the first forward
         # also lays the direction parameters out in their stacked buffers
         side = torch.cuda.Stream(device)
@@ -142,14 +138,30 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
         issued = time.perf_counter() - t0
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        if not math.isfinite(float(gloss.detach())):
-            raise RuntimeError("non-finite loss")
-        value_region = {"elapsed": elapsed, "issued": issued}
+        return {"elapsed": elapsed, "issued": issued}, gloss
+
+    mode = "graph" if graph else "eager"
+    if graph:
+        try:
+            value_region, gloss = graph_region()
+            if not math.isfinite(float(gloss.detach())):
+                raise FloatingPointError("non-finite loss in the captured step")
+        except RuntimeError as err:  # capture refused: time the eager loop
+            print(f"bench.py: HIP graph capture failed ({err}); timing the eager loop",
+                  file=sys.stderr, flush=True)
+            torch.cuda.synchronize()
+            mode, graph = "eager (graph capture failed)", False
+    if not graph:
+        for _ in range(warmup):
+            step(opt_eager)
+        region, records = eager_region()
+        value_region = region
+    else:
         region, records = eager_region()
     per = {"fwd": [], "bwd": []}
     for kind, e0, e1, nbytes in records:
         per[kind].append((e0.elapsed_time(e1) * 1e-3, nbytes))
-    return value_region, region, per
+    return value_region, region, per, mode
 
 
 def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
@@ -351,8 +363,8 @@ def main():
         print(json.dumps({"tuned_gemms": args.tune_gemms}), flush=True)
         return
     tuned = False if args.default_gemms else gemm_tuning.load()
-    value_region, eager, per = bench_step(torch, mvm, scan, args.steps, args.warmup, device,
-                                          graph=not args.eager)
+    value_region, eager, per, mode = bench_step(torch, mvm, scan, args.steps, args.warmup, device,
+                                                graph=not args.eager)
     elapsed, enqueued = value_region["elapsed"], value_region["issued"]
     imgs = 32 * args.steps / elapsed
 
@@ -387,7 +399,7 @@ def main():
         # host time to issue one step (python, autograd, launches): the step
         # is host-bound when this approaches ms_per_step
         "host_issue_ms_per_step": round(enqueued / args.steps * 1e3, 3),
-        "execution": "eager" if args.eager else "HIP graph replay of the captured step",
+        "execution": "HIP graph replay of the captured step" if mode == "graph" else mode,
         "eager_ms_per_step": round(eager["elapsed"] / args.steps * 1e3, 3),
         "eager_host_issue_ms_per_step": round(eager["issued"] / args.steps * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
