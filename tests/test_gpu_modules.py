@@ -57,7 +57,8 @@ def _compare_grads(module, params):
         _compare(f"grad {n}", p.grad, params[n].grad)
 
 
-@pytest.mark.parametrize("mode", ["sequential", "chunked", "hip", "metal_fused"])
+@pytest.mark.parametrize("mode", ["sequential", "chunked", "hip", "metal_fused", "parallel",
+                                  "metal_train"])
 def test_mamba_block(cuda, mode):
     torch.manual_seed(0)
     blk = mvm.MambaBlock(d_model=32, d_state=16, scan_mode=mode)
@@ -232,3 +233,22 @@ def test_graph_captured_step_matches_eager(cuda):
         assert torch.allclose(gloss.detach(), eloss.detach(), rtol=1e-6, atol=0), i
         for (n, p), (_, q) in zip(mg.named_parameters(), me.named_parameters()):
             assert torch.allclose(p, q, rtol=1e-5, atol=1e-7), (i, n)
+
+
+def test_metal_mode_is_forward_only(cuda):
+    """scan_mode "metal" is the reference's inference-only scan
+    (mamba_metal.py:230): the output matches the oracle, and a backward
+    reaches only out_proj (the block core is detached)."""
+    torch.manual_seed(12)
+    blk = mvm.MambaBlock(d_model=32, d_state=16, scan_mode="metal").to(cuda)
+    x = torch.randn(2, 23, 32)
+    y = blk(x.to(cuda))
+    params = torch_ref.params_from_module(blk)
+    with torch.no_grad():
+        yr = torch_ref.mamba_block(params, "", x.double(), 16, 4)
+    _compare("output", y, yr)
+    y.sum().backward()
+    assert blk.out_proj.weight.grad is not None
+    for name in ("in_proj", "x_proj", "dt_proj", "conv1d"):
+        assert getattr(blk, name).weight.grad is None, name
+    assert blk.A_log.grad is None and blk.D.grad is None
