@@ -507,13 +507,17 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 // token row each scan position read (mamba_metal_fused.py:221,224).
 template <typename OT>
 __device__ __forceinline__ void reduce_bc_part(const Geom& gm, const BwdBufs& bf, int64_t blk) {
-  const int64_t idx = blk * kThreads + threadIdx.x;
-  const int64_t total = gm.B * gm.K * gm.L * 2 * kStatePad;
-  if (idx >= total) return;
-  const int n = static_cast<int>(idx % kStatePad);
-  const int w2 = static_cast<int>((idx / kStatePad) & 1);
-  const int64_t t = (idx / (2 * kStatePad)) % gm.L;
-  const int64_t bk = idx / (2 * kStatePad * gm.L);
+  static_assert(kStatePad == 16, "the (t, dB|dC, n) index below is a bit split");
+  // blocks of one (batch, direction) row cover its L x 32 outputs; the
+  // division is block-uniform (scalar), the split of j is shifts and masks
+  const int64_t row_elems = gm.L * 2 * kStatePad;
+  const int64_t bpr = (row_elems + kThreads - 1) / kThreads;
+  const int64_t bk = blk / bpr;
+  const int64_t j = (blk - bk * bpr) * kThreads + threadIdx.x;
+  if (j >= row_elems) return;
+  const int n = static_cast<int>(j & 15);
+  const int w2 = static_cast<int>((j >> 4) & 1);
+  const int64_t t = j >> 5;
   if (n >= gm.N) return;
   // the channel-block partials are summed left to right; unrolled so that
   // their loads are in flight together
@@ -522,7 +526,7 @@ __device__ __forceinline__ void reduce_bc_part(const Geom& gm, const BwdBufs& bf
   float s = 0.f;
 #pragma unroll 4
   for (int64_t cb = 0; cb < gm.ncblk; ++cb) s += pp[cb * cstride];
-  const int64_t b = bk / gm.K, k = bk % gm.K;
+  const int64_t b = bk / gm.K, k = bk - b * gm.K;
   const int64_t row = token_row(gm.tok ? gm.tok + k * gm.L : nullptr, t, gm.L);
   OT* out = static_cast<OT*>(w2 ? bf.dC : bf.dB);
   st(out, b * gm.bsb + k * gm.bsk + row * gm.bst + n, s);
@@ -559,11 +563,16 @@ __device__ __forceinline__ void reduce_ad_part(const Geom& gm, const BwdBufs& bf
   const int64_t per = (nparts + 3) / 4;
   const int64_t q0 = wave * per, q1 = min(nparts, q0 + per);
   double s = 0.0;
-  if (valid) {
+  if (valid && q0 < q1) {
+    // q = b * nchunk + c, stepped without a division per partial
+    int64_t b = q0 / gm.nchunk, c = q0 - b * gm.nchunk;
     for (int64_t q = q0; q < q1; ++q) {
-      const int64_t b = q / gm.nchunk, c = q - (q / gm.nchunk) * gm.nchunk;
       const int64_t slot = ((b * gm.K + k) * gm.nchunk + c) * gm.D + d;
       s += kind == 0 ? bf.part_dA[slot * kStatePad + n] : (kind == 1 ? bf.part_dD[slot] : bf.part_db[slot]);
+      if (++c == gm.nchunk) {
+        c = 0;
+        ++b;
+      }
     }
   }
   sq[wave][lane] = s;
@@ -614,7 +623,7 @@ static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) 
     hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, true>), grid, block, 0, s, g, b);
   else
     hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, false>), grid, block, 0, s, g, b);
-  const int64_t nbc_blocks = (g.B * g.K * g.L * 2 * kStatePad + kThreads - 1) / kThreads;
+  const int64_t nbc_blocks = g.B * g.K * ((g.L * 2 * kStatePad + kThreads - 1) / kThreads);
   const int64_t nad_blocks = (g.K * g.D * (kStatePad + 2) + 63) / 64;
   hipLaunchKernelGGL((reduce_grads_kernel<OT>), dim3(static_cast<unsigned>(nbc_blocks + nad_blocks)),
                      block, 0, s, g, b, nbc_blocks);
