@@ -37,7 +37,9 @@ so its HBM fraction follows from its instruction count).
 
 scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
 D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads,
-timed over back-to-back calls with inputs resident in HBM.
+timed over back-to-back calls with inputs resident in HBM (events split
+the stream time between forward and VJP), and as replays of the pair
+captured in a HIP graph (graph_fwd_vjp_us: no host time between launches).
 
 cpu_baseline: the oracle's CPU restatement of the reference's sequential
 VisionMamba step (materialised discretisation, Python time loop, autograd)
@@ -191,7 +193,7 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
     size = 2 if dtype == torch.bfloat16 else 4
     bf, bb = scan.algorithmic_bytes(bsz, L, D, N, size, size)
     total = tf + tb
-    return {
+    out = {
         "shape": f"B={bsz} L={L} D={D} N={N} {'bf16' if size == 2 else 'fp32'}",
         "fwd_us": round(tf * 1e6, 2), "vjp_us": round(tb * 1e6, 2),
         "algorithmic_bytes": bf + bb,
@@ -199,6 +201,33 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
         "pct_hbm_peak": round((bf + bb) / total / 1e9 / HBM_PEAK_GBS * 100, 2),
         "tokens_per_s": round(bsz * L / total, 1),
     }
+    # the same fwd + VJP pair replayed from a captured HIP graph: no host
+    # work between the launches, so this is the GPU time of the pair (at
+    # small shapes the eager calls above also hold the host's launch time)
+    try:
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            y, ck = scan.scan_forward(*args, save_ckpt=True)
+            scan.scan_backward(*args, g4, ckpt=ck)
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y, ck = scan.scan_forward(*args, save_ckpt=True)
+            scan.scan_backward(*args, g4, ckpt=ck)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            graph.replay()
+        torch.cuda.synchronize()
+        tg = (time.perf_counter() - t0) / iters
+        out["graph_fwd_vjp_us"] = round(tg * 1e6, 2)
+        out["graph_GBps"] = round((bf + bb) / tg / 1e9, 1)
+    except RuntimeError as err:
+        print(f"bench.py: scan graph capture failed ({err})", file=sys.stderr, flush=True)
+    return out
 
 
 def step_scan_inputs(torch, device):
