@@ -120,6 +120,24 @@ def test_small_workspace_rejected_before_launch():
     assert "workspace" in _lib.last_error()
 
 
+@pytest.mark.parametrize("B,L,D", [(0, 40, 24), (2, 0, 24), (2, 40, 0)])
+def test_empty_forward_is_a_no_op(B, L, D):
+    """An empty (b, t, d) range needs no buffers: the forward validates and
+    returns before any launch, with NULL tensor pointers and no workspace."""
+    lib = _lib.lib()
+    d = _desc(B=B, L=L, D=D)
+    assert lib.mvm_scan_validate(ctypes.byref(d)) == _lib.MVM_OK
+    assert lib.mvm_scan_ckpt_elems(ctypes.byref(d)) == 0
+    assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), 0) == 0
+    assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), 1) >= 0
+    null = ctypes.c_void_p(0)
+    assert lib.mvm_scan_fwd(ctypes.byref(d), *([null] * 9), 0, null) == _lib.MVM_OK
+    # the backward still owes dA and dD (zero sums over the empty range)
+    if D > 0:
+        assert lib.mvm_scan_bwd(ctypes.byref(d), *([null] * 15), 0, null) == _lib.MVM_ERR_INVALID_ARG
+        assert "dA" in _lib.last_error()
+
+
 def test_null_desc():
     assert _lib.lib().mvm_scan_validate(None) == _lib.MVM_ERR_INVALID_ARG
 

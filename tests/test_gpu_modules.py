@@ -252,3 +252,23 @@ def test_metal_mode_is_forward_only(cuda):
     for name in ("in_proj", "x_proj", "dt_proj", "conv1d"):
         assert getattr(blk, name).weight.grad is None, name
     assert blk.A_log.grad is None and blk.D.grad is None
+
+
+def test_block_with_no_tokens(cuda):
+    """A MambaBlock over an empty token axis: an empty output, and every
+    parameter gradient (all of them sums over tokens) exactly zero."""
+    print("case: MambaBlock with 0 tokens", flush=True)
+    torch.manual_seed(5)
+    blk = mvm.MambaBlock(d_model=32, d_state=16, scan_mode="metal_fused").to(cuda)
+    x = torch.randn(2, 0, 32, device=cuda, requires_grad=True)
+    # NaN garbage in the allocator: a gradient nobody writes would show
+    junk = [torch.full((n,), float("nan"), device=cuda) for n in (64, 64 * 4, 64 * 16) for _ in range(64)]
+    del junk
+    y = blk(x)
+    assert y.shape == (2, 0, 32)
+    y.sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == x.shape
+    for name, p in blk.named_parameters():
+        assert p.grad is not None, name
+        assert torch.equal(p.grad, torch.zeros_like(p)), name

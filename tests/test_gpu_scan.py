@@ -239,3 +239,35 @@ def test_full_long_sequence_properties(cuda):
     assert_close(y3, y1.cpu().double().numpy(), "y (chunk 4096 vs auto)")
     for name, a, b in zip(NAMES, g3, g1):
         assert_close(a, b.cpu().double().numpy(), f"{name} (chunk 4096 vs auto)", atol=1e-4, rtol=1e-3)
+
+
+def _dirty_small_pool(device, numel, count=256):
+    """Leave NaN-filled blocks of `numel` floats in the caching allocator so
+    that an output the library fails to write reads back as NaN, not 0."""
+    junk = [torch.full((numel,), float("nan"), device=device) for _ in range(count)]
+    del junk
+
+
+@pytest.mark.parametrize("bsz,L", [(0, 24), (2, 0)])
+def test_empty_batch_or_sequence(cuda, bsz, L):
+    """Sums over an empty (b, t) range: dA and dD come back as exact zeros,
+    every other tensor is empty with its primal's shape."""
+    from mlx_vision_mamba_amd import scan
+    print(f"case: empty scan B={bsz} L={L}", flush=True)
+    D, N = 32, 16
+    u = torch.randn(bsz, L, D, device=cuda, requires_grad=True)
+    dl = torch.rand(bsz, L, D, device=cuda, requires_grad=True)
+    A = (-torch.arange(1, N + 1, dtype=torch.float32)).repeat(D, 1).to(cuda).requires_grad_(True)
+    Bm = torch.randn(bsz, L, N, device=cuda, requires_grad=True)
+    Cm = torch.randn(bsz, L, N, device=cuda, requires_grad=True)
+    Dv = torch.ones(D, device=cuda, requires_grad=True)
+    y = scan.selective_scan(u, dl, A, Bm, Cm, Dv)
+    assert y.shape == (bsz, L, D)
+    _dirty_small_pool(cuda, D * N)
+    _dirty_small_pool(cuda, D)
+    grads = torch.autograd.grad(y, [u, dl, A, Bm, Cm, Dv], torch.randn_like(y))
+    torch.cuda.synchronize()
+    for g, p in zip(grads, (u, dl, A, Bm, Cm, Dv)):
+        assert g.shape == p.shape
+    assert torch.equal(grads[2], torch.zeros_like(A))
+    assert torch.equal(grads[5], torch.zeros_like(Dv))
