@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define MVM_ABI_VERSION 3
+#define MVM_ABI_VERSION 4
 
 /* status codes */
 #define MVM_OK 0

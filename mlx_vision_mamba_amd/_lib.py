@@ -24,7 +24,8 @@ MVM_ERR_HIP = -4
 MVM_F32 = 0
 MVM_BF16 = 1
 MVM_MAX_DSTATE = 16
-ABI_VERSION = 3
+ABI_VERSION = 4
+MVM_NORM_MAX_COLS = 1024
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -67,8 +68,18 @@ class ConvDesc(ctypes.Structure):
     ]
 
 
+class NormDesc(ctypes.Structure):
+    """Mirror of ``mvm_norm_desc`` (include/mvm_norm.h)."""
+
+    _fields_ = [
+        ("rows", _i64), ("cols", _i64), ("x_stride", _i64), ("y_stride", _i64),
+        ("eps", ctypes.c_float), ("reserved", _i32),
+    ]
+
+
 # symbol -> (restype, argtypes); every entry point of include/mvm_scan.h,
-# include/mvm_conv.h and the test hook of include/mvm_testing.h
+# include/mvm_conv.h, include/mvm_norm.h and the test hook of
+# include/mvm_testing.h
 SIGNATURES = {
     "mvm_abi_version": (ctypes.c_int, []),
     "mvm_last_error": (ctypes.c_char_p, []),
@@ -86,6 +97,10 @@ SIGNATURES = {
     "mvm_conv_workspace_bytes": (_i64, [ctypes.POINTER(ConvDesc)]),
     "mvm_conv_silu_fwd": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [_vp] * 5),
     "mvm_conv_silu_bwd": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [_vp] * 8 + [ctypes.c_size_t, _vp]),
+    "mvm_norm_validate": (ctypes.c_int, [ctypes.POINTER(NormDesc)]),
+    "mvm_norm_workspace_bytes": (_i64, [ctypes.POINTER(NormDesc)]),
+    "mvm_layernorm_fwd": (ctypes.c_int, [ctypes.POINTER(NormDesc)] + [_vp] * 7),
+    "mvm_layernorm_bwd": (ctypes.c_int, [ctypes.POINTER(NormDesc)] + [_vp] * 10 + [ctypes.c_size_t, _vp]),
     "mvm_selftest_lanes": (ctypes.c_int, [_vp, _vp]),
 }
 

@@ -1,4 +1,5 @@
-// C ABI of libmvm_scan.so (declared in include/mvm_scan.h).
+// C ABI of libmvm_scan.so (declared in include/mvm_scan.h, mvm_conv.h and
+// mvm_norm.h).
 //
 // Host-side responsibilities: validate every argument before anything is
 // enqueued, pick the time-chunk length, carve the caller's workspace into
@@ -12,6 +13,8 @@
 
 #include "conv_kernels.h"
 #include "mvm_conv.h"
+#include "mvm_norm.h"
+#include "norm_kernels.h"
 #include "mvm_scan.h"
 #include "mvm_testing.h"
 #include "scan_common.h"
@@ -536,6 +539,84 @@ int mvm_conv_silu_bwd(const mvm_conv_desc* desc, const float* x, const float* w,
 int mvm_selftest_lanes(float* out, void* stream) {
   if (out == nullptr) return fail(MVM_ERR_INVALID_ARG, "out is NULL");
   return hip_status(mvm::launch_selftest_lanes(out, static_cast<hipStream_t>(stream)), "selftest");
+}
+
+}  // extern "C"
+
+namespace {
+
+// MVM_NORM_MAX_ROWS: the forward's grid (4 rows per 256-thread workgroup)
+// stays below 2^31 threads
+constexpr int64_t kNormMaxRows = MVM_NORM_MAX_ROWS;
+
+int check_norm(const mvm_norm_desc* d) {
+  if (d == nullptr) return fail(MVM_ERR_INVALID_ARG, "norm desc is NULL");
+  if (d->rows < 0) return fail(MVM_ERR_INVALID_ARG, "norm rows=%lld < 0", (long long)d->rows);
+  if (d->rows > kNormMaxRows)
+    return fail(MVM_ERR_UNSUPPORTED, "norm rows=%lld exceeds %lld", (long long)d->rows,
+                (long long)kNormMaxRows);
+  if (d->cols < 1 || d->cols > MVM_NORM_MAX_COLS)
+    return fail(MVM_ERR_UNSUPPORTED, "norm cols=%lld unsupported (1..%d)", (long long)d->cols,
+                MVM_NORM_MAX_COLS);
+  if (d->x_stride < d->cols || d->y_stride < d->cols)
+    return fail(MVM_ERR_INVALID_ARG, "norm row strides must be >= cols");
+  if (!(d->eps >= 0.f) || d->eps > 1e30f)
+    return fail(MVM_ERR_INVALID_ARG, "norm eps must be finite and >= 0");
+  if (d->reserved != 0) return fail(MVM_ERR_INVALID_ARG, "norm desc reserved field must be 0");
+  return MVM_OK;
+}
+
+mvm::NormGeom norm_geom(const mvm_norm_desc* d) {
+  mvm::NormGeom g;
+  g.rows = d->rows; g.cols = d->cols; g.xs = d->x_stride; g.ys = d->y_stride; g.eps = d->eps;
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvm_norm_validate(const mvm_norm_desc* desc) {
+  const int rc = check_norm(desc);
+  return rc == MVM_OK ? ok() : rc;
+}
+
+int64_t mvm_norm_workspace_bytes(const mvm_norm_desc* desc) {
+  const int rc = check_norm(desc);
+  if (rc != MVM_OK) return rc;
+  return static_cast<int64_t>(align_up(sizeof(float) * mvm::norm_partial_floats(norm_geom(desc))));
+}
+
+int mvm_layernorm_fwd(const mvm_norm_desc* desc, const float* x, const float* gamma,
+                      const float* beta, float* y, float* mean, float* rstd, void* stream) {
+  const int rc = check_norm(desc);
+  if (rc != MVM_OK) return rc;
+  if (desc->rows == 0) return ok();
+  if (!x || !gamma || !beta || !y || !mean || !rstd)
+    return fail(MVM_ERR_INVALID_ARG, "mvm_layernorm_fwd: NULL pointer");
+  return hip_status(mvm::launch_norm_fwd(norm_geom(desc), x, gamma, beta, y, mean, rstd,
+                                         static_cast<hipStream_t>(stream)),
+                    "mvm_layernorm_fwd launch");
+}
+
+int mvm_layernorm_bwd(const mvm_norm_desc* desc, const float* x, const float* gamma,
+                      const float* mean, const float* rstd, const float* dy, const float* dres,
+                      float* dx, float* dgamma, float* dbeta, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  int rc = check_norm(desc);
+  if (rc != MVM_OK) return rc;
+  if (!gamma || !dgamma || !dbeta)
+    return fail(MVM_ERR_INVALID_ARG, "mvm_layernorm_bwd: NULL gamma, dgamma or dbeta");
+  if (desc->rows > 0 && (!x || !mean || !rstd || !dy || !dx))
+    return fail(MVM_ERR_INVALID_ARG, "mvm_layernorm_bwd: NULL pointer");
+  const mvm::NormGeom g = norm_geom(desc);
+  rc = check_ws("mvm_layernorm_bwd", workspace, workspace_bytes,
+                align_up(sizeof(float) * mvm::norm_partial_floats(g)));
+  if (rc != MVM_OK) return rc;
+  return hip_status(mvm::launch_norm_bwd(g, x, gamma, mean, rstd, dy, dres, dx, dgamma, dbeta,
+                                         static_cast<float*>(workspace),
+                                         static_cast<hipStream_t>(stream)),
+                    "mvm_layernorm_bwd launch");
 }
 
 }  // extern "C"

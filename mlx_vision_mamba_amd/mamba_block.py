@@ -44,6 +44,7 @@ import torch.nn.functional as F
 
 from . import directions as _dirs
 from .conv import conv_silu_backward_into, conv_silu_forward_into
+from .norm import layer_norm
 from .scan import get_scan_fn, mode_chunk_len, scan_fused_backward, scan_fused_forward
 
 
@@ -98,7 +99,8 @@ class ResidualMambaBlock(nn.Module):
         self.mamba = MambaBlock(d_model, d_state, d_conv, expand_factor, scan_mode)
 
     def forward(self, x):
-        return x + self.mamba(self.norm(x))
+        h, xr = layer_norm(x, self.norm, residual=True)
+        return xr + self.mamba(h)
 
 
 class BidirectionalMambaBlock(nn.Module):
@@ -115,11 +117,11 @@ class BidirectionalMambaBlock(nn.Module):
         self._tables = {}
 
     def forward(self, x):
-        h = self.norm(x)
+        h, xr = layer_norm(x, self.norm, residual=True)                      # :227
         tok = _cached_table(self._tables, 2, x.shape[1], None, x.device)
         blocks = [self.forward_mamba, self.backward_mamba]
-        return x + _directional_forward(blocks, h, tok, self.scan_mode,
-                                        _direction_stacks(self, blocks))
+        return xr + _directional_forward(blocks, h, tok, self.scan_mode,
+                                         _direction_stacks(self, blocks))
 
 
 class MultiDirectionalMambaBlock(nn.Module):
@@ -151,7 +153,7 @@ class MultiDirectionalMambaBlock(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         bsz, n, _ = x.shape
-        h = self.norm(x)                                                       # :548
+        h, xr = layer_norm(x, self.norm, residual=True)                      # :548
         expected = math.prod(self.grid_shape) if self.grid_shape is not None else n
         stacks = _direction_stacks(self, list(self.mamba_blocks))
         if n != expected and self.num_directions > 2:                         # :554-559
@@ -161,7 +163,7 @@ class MultiDirectionalMambaBlock(nn.Module):
             grid = self.grid_shape if self.num_directions > 2 else None
             tok = _cached_table(self._tables, self.num_directions, n, grid, x.device)
             blocks = list(self.mamba_blocks)
-        return x + _directional_forward(blocks, h, tok, self.scan_mode, stacks)  # :562-566
+        return xr + _directional_forward(blocks, h, tok, self.scan_mode, stacks)  # :562-566
 
 
 # per-direction parameters stored as slices of one (K, ...) buffer per kind

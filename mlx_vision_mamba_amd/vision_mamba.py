@@ -15,6 +15,7 @@ import torch
 import torch.nn as nn
 
 from .mamba_block import MultiDirectionalMambaBlock
+from .norm import layer_norm
 from .vit import PatchEmbed, PatchEmbed3D, embed_3d
 
 
@@ -93,7 +94,7 @@ class VisionMamba(nn.Module):
             x = x + self.pos_embed
         for block in self.blocks:                                      # :220-221
             x = block(x)
-        return self.norm(x)                                            # :223
+        return layer_norm(x, self.norm)                                # :223
 
     def embed_patches(self, images: torch.Tensor) -> torch.Tensor:
         return self.patch_embed(images)                                # :226-228

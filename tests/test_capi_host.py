@@ -19,7 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared_functions():
     names = []
-    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(", text)
@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 def _header_arity():
     """Parameter count of every function declared in the headers."""
     out = {}
-    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for name, params in re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
@@ -287,3 +287,63 @@ def test_fused_null_pointers_rejected_before_launch():
     bargs = [fake] * 20
     bargs[9 + 1] = null  # ckpt
     assert lib.mvm_scan_fused_bwd(ctypes.byref(fd), *bargs, need, null) == _lib.MVM_ERR_INVALID_ARG
+
+
+def _norm_desc(rows=100, cols=384, xs=None, ys=None, eps=1e-5):
+    d = _lib.NormDesc()
+    d.rows, d.cols = rows, cols
+    d.x_stride = cols if xs is None else xs
+    d.y_stride = cols if ys is None else ys
+    d.eps = eps
+    d.reserved = 0
+    return d
+
+
+def test_norm_desc_layout_matches_header():
+    # int64 x4, float, int32: 40 bytes, no padding
+    assert ctypes.sizeof(_lib.NormDesc) == 40
+    assert _lib.NormDesc.eps.offset == 32 and _lib.NormDesc.reserved.offset == 36
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("rows", -1, _lib.MVM_ERR_INVALID_ARG),
+    ("rows", (1 << 25) + 1, _lib.MVM_ERR_UNSUPPORTED),
+    ("cols", 0, _lib.MVM_ERR_UNSUPPORTED),
+    ("cols", _lib.MVM_NORM_MAX_COLS + 1, _lib.MVM_ERR_UNSUPPORTED),
+    ("x_stride", 383, _lib.MVM_ERR_INVALID_ARG),
+    ("y_stride", 100, _lib.MVM_ERR_INVALID_ARG),
+    ("eps", -1e-5, _lib.MVM_ERR_INVALID_ARG),
+    ("eps", float("nan"), _lib.MVM_ERR_INVALID_ARG),
+    ("eps", float("inf"), _lib.MVM_ERR_INVALID_ARG),
+    ("reserved", 1, _lib.MVM_ERR_INVALID_ARG),
+])
+def test_norm_bad_descriptors_rejected(field, value, code):
+    lib = _lib.lib()
+    d = _norm_desc()
+    assert lib.mvm_norm_validate(ctypes.byref(d)) == _lib.MVM_OK
+    setattr(d, field, value)
+    assert lib.mvm_norm_validate(ctypes.byref(d)) == code
+    assert _lib.last_error() != ""
+    assert lib.mvm_norm_workspace_bytes(ctypes.byref(d)) == code
+
+
+def test_norm_workspace_and_host_checks():
+    lib = _lib.lib()
+    null = ctypes.c_void_p(0)
+    # one partial row (2 * cols floats) per backward workgroup (8 rows per
+    # workgroup pass), <= 256 of them
+    for rows, blocks in ((1, 1), (16, 2), (6272, 256), (0, 1)):
+        d = _norm_desc(rows=rows)
+        need = lib.mvm_norm_workspace_bytes(ctypes.byref(d))
+        assert need >= blocks * 2 * 384 * 4 and need % 256 == 0 and need - blocks * 2 * 384 * 4 < 256
+    d = _norm_desc(rows=0)
+    # an empty forward needs no buffers and launches nothing
+    assert lib.mvm_layernorm_fwd(ctypes.byref(d), *([null] * 6), null) == _lib.MVM_OK
+    d = _norm_desc(rows=10)
+    assert lib.mvm_layernorm_fwd(ctypes.byref(d), *([null] * 6), null) == _lib.MVM_ERR_INVALID_ARG
+    assert "NULL" in _lib.last_error()
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+    need = lib.mvm_norm_workspace_bytes(ctypes.byref(d))
+    assert lib.mvm_layernorm_bwd(ctypes.byref(d), *([fake] * 10), need - 1, null) == _lib.MVM_ERR_WORKSPACE
+    assert lib.mvm_layernorm_bwd(ctypes.byref(d), fake, fake, fake, fake, fake, null, fake, null, fake,
+                                 fake, need, null) == _lib.MVM_ERR_INVALID_ARG
