@@ -34,6 +34,11 @@ reads for a 512 MiB copy (committed summary in profiles/, made with
 valu_busy_per_simd: the share of that kernel's time its SIMDs' VALU is busy,
 from the SQ counters of the same summary (the backward is bound by VALU issue,
 so its HBM fraction follows from its instruction count).
+secondary_flops: the reference formula's work, 37 flop + 3 exp per
+(b, t, d, n) element for forward + VJP (mamba_metal_fused.py:33-145), over the
+mean fused forward + backward call time, against the 157.3 TFLOP/s fp32
+vector peak (reported, not the bound; the scan-only entries carry the same
+rate as ref_formula_TFLOPs).
 
 scan: the scan alone (forward + VJP through the C ABI) at B=2, L=196,
 D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads,
@@ -61,6 +66,11 @@ if ROOT not in sys.path:
 
 METRIC = "selective-scan fwd+VJP GB/s & % HBM peak; VisionMamba-2D train imgs/sec"
 HBM_PEAK_GBS = 8000.0
+# the reference formula's work per (b, t, d, n) element for forward + VJP
+# (mamba_metal_fused.py:33-145), against the MI355X fp32 vector peak
+REF_FLOP_PER_ELEMENT = 37
+REF_EXP_PER_ELEMENT = 3
+FP32_VECTOR_PEAK_TFLOPS = 157.3
 BWD_KERNELS = ("mvm_scan_fused_bwd: scan_bwd_kernel<float, float, fused> + reduce_grads_kernel "
                "(one time chunk at this shape, so no aggregate pass)")
 
@@ -166,6 +176,17 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     return value_region, region, per, mode
 
 
+def secondary_flops(elements, seconds):
+    """The reference formula's work (REF_FLOP_PER_ELEMENT flop and
+    REF_EXP_PER_ELEMENT exp per (b, t, d, n), forward + VJP) over a measured
+    fwd + VJP time, against the fp32 vector peak."""
+    tflops = REF_FLOP_PER_ELEMENT * elements / seconds / 1e12
+    return {"flop_per_element": REF_FLOP_PER_ELEMENT, "exp_per_element": REF_EXP_PER_ELEMENT,
+            "elements": elements, "fwd_plus_vjp_us": round(seconds * 1e6, 2),
+            "achieved_TFLOPs": round(tflops, 2), "peak_TFLOPs": FP32_VECTOR_PEAK_TFLOPS,
+            "frac": round(tflops / FP32_VECTOR_PEAK_TFLOPS, 4)}
+
+
 def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
     from tests import scan_inputs
     u, dl, A, Bm, Cm, Dv, g = [t.to(device) for t in scan_inputs.make(bsz, L, D, N, seed=0,
@@ -200,6 +221,8 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
         "GBps": round((bf + bb) / total / 1e9, 1),
         "pct_hbm_peak": round((bf + bb) / total / 1e9 / HBM_PEAK_GBS * 100, 2),
         "tokens_per_s": round(bsz * L / total, 1),
+        # secondary: reference-formula flop rate of the fwd + VJP pair
+        "ref_formula_TFLOPs": round(REF_FLOP_PER_ELEMENT * bsz * L * D * N / total / 1e12, 3),
     }
     # the same fwd + VJP pair replayed from a captured HIP graph: no host
     # work between the launches, so this is the GPU time of the pair (at
@@ -416,6 +439,9 @@ def main():
         # the backward is VALU-issue bound: share of the kernel's time the
         # SIMDs' VALU is busy (SQ counters, committed profile)
         "valu_busy_per_simd": measured_traffic("bwd_valu_busy_per_simd", float),
+        # secondary: the reference formula's flop rate over the fused fwd +
+        # VJP calls (B*K = 128 scans of L = 196, D = 768, N = 16)
+        "secondary_flops": secondary_flops(32 * 4 * 196 * 768 * 16, fwd_t + bwd_t),
     }
     scans = {
         "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 200, device),

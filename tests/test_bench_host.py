@@ -29,6 +29,17 @@ def test_algorithmic_bytes_of_the_measured_calls():
     assert vjp == 4 * (8 * BLD + 4 * BLN) + 4 * (768 * 16 * 8 + 768 * 8 + 768 * 8)
 
 
+def test_secondary_flop_rate():
+    # 37 flop per element (forward + VJP of the reference formula): 1e9
+    # elements in 1 ms is 37 TFLOP/s, 23.5 % of the 157.3 TFLOP/s fp32 peak
+    sec = bench.secondary_flops(1_000_000_000, 1e-3)
+    assert sec["achieved_TFLOPs"] == 37.0
+    assert abs(sec["frac"] - 37.0 / 157.3) < 1e-4
+    assert sec["flop_per_element"] == 37 and sec["exp_per_element"] == 3
+    # the VisionMamba step's fused calls: B*K = 128 scans of 196 x 768 x 16
+    assert 32 * 4 * 196 * 768 * 16 == 308_281_344
+
+
 def test_profile_figures_read_by_the_bench():
     traffic = bench.measured_traffic("bwd_call_hbm_bytes")
     assert isinstance(traffic, int)
