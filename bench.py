@@ -31,9 +31,9 @@ peak of 8 TB/s.  traffic = HBM bytes per backward call at this shape from
 the rocprofv3 FETCH_SIZE and WRITE_SIZE counters, each scaled by what it
 reads for a 512 MiB copy (committed summary in profiles/, made with
 `bench.py --scan-driver`), or null when that summary is absent.
-valu_busy_per_simd: the share of that kernel's time its SIMDs' VALU is busy,
-from the SQ counters of the same summary (the backward is bound by VALU issue,
-so its HBM fraction follows from its instruction count).
+valu_busy_per_simd: the share of that kernel's cycles its SIMDs' VALU is
+issuing, rocprofv3's VALUBusy counter in the same summary (the backward is
+bound by VALU issue, so its HBM fraction follows from its instruction count).
 secondary_flops: the reference formula's work, 37 flop + 3 exp per
 (b, t, d, n) element for forward + VJP (mamba_metal_fused.py:33-145), over the
 mean fused forward + backward call time, against the 157.3 TFLOP/s fp32
@@ -311,7 +311,7 @@ def measured_traffic(key, kind=int):
     """A figure measured with rocprofv3 counters on the scan at the
     VisionMamba step shape (a line `key: <value>` of the committed profile
     summary: HBM bytes per call from FETCH_SIZE / WRITE_SIZE, or the
-    backward's VALU busy fraction from the SQ counters), or None."""
+    backward's VALU busy fraction from the VALUBusy counter), or None."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
@@ -437,7 +437,7 @@ def main():
         "fwd_call": {"achieved": round(fwd_b / fwd_t / 1e9, 1), "avg_launch_us": round(fwd_t * 1e6, 2),
                      "algorithmic_bytes_per_launch": int(fwd_b)},
         # the backward is VALU-issue bound: share of the kernel's time the
-        # SIMDs' VALU is busy (SQ counters, committed profile)
+        # SIMDs' VALU is issuing (VALUBusy counter, committed profile)
         "valu_busy_per_simd": measured_traffic("bwd_valu_busy_per_simd", float),
         # secondary: the reference formula's flop rate over the fused fwd +
         # VJP calls (B*K = 128 scans of L = 196, D = 768, N = 16)
