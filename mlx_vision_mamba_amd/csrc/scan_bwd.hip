@@ -519,13 +519,20 @@ __device__ __forceinline__ void reduce_bc_part(const Geom& gm, const BwdBufs& bf
   const int w2 = static_cast<int>((j >> 4) & 1);
   const int64_t t = j >> 5;
   if (n >= gm.N) return;
-  // the channel-block partials are summed left to right; unrolled so that
-  // their loads are in flight together
+  // the channel-block partials are summed left to right; each batch's
+  // loads are in flight together (the bounds are block-uniform)
   const float* pp = bf.part_bc + (bk * gm.ncblk * gm.L + t) * (2 * kStatePad) + w2 * kStatePad + n;
   const int64_t cstride = gm.L * 2 * kStatePad;
+  constexpr int kBatch = 16;
   float s = 0.f;
-#pragma unroll 4
-  for (int64_t cb = 0; cb < gm.ncblk; ++cb) s += pp[cb * cstride];
+  for (int64_t cb0 = 0; cb0 < gm.ncblk; cb0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = cb0 + u < gm.ncblk ? pp[(cb0 + u) * cstride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (cb0 + u < gm.ncblk) s += v[u];
+  }
   const int64_t b = bk / gm.K, k = bk - b * gm.K;
   const int64_t row = token_row(gm.tok ? gm.tok + k * gm.L : nullptr, t, gm.L);
   OT* out = static_cast<OT*>(w2 ? bf.dC : bf.dB);
@@ -564,15 +571,31 @@ __device__ __forceinline__ void reduce_ad_part(const Geom& gm, const BwdBufs& bf
   const int64_t q0 = wave * per, q1 = min(nparts, q0 + per);
   double s = 0.0;
   if (valid && q0 < q1) {
-    // q = b * nchunk + c, stepped without a division per partial
+    // the lane's partial array: element (slot) at src[slot * smul + n]
+    const double* src = kind == 0 ? bf.part_dA : (kind == 1 ? bf.part_dD : bf.part_db);
+    const int64_t smul = kind == 0 ? kStatePad : 1;
+    const int64_t sadd = kind == 0 ? n : 0;
+    // q = b * nchunk + c, stepped without a division per partial; each
+    // batch's loads are in flight together, then added in partial order
+    constexpr int kBatch = 8;
     int64_t b = q0 / gm.nchunk, c = q0 - b * gm.nchunk;
-    for (int64_t q = q0; q < q1; ++q) {
-      const int64_t slot = ((b * gm.K + k) * gm.nchunk + c) * gm.D + d;
-      s += kind == 0 ? bf.part_dA[slot * kStatePad + n] : (kind == 1 ? bf.part_dD[slot] : bf.part_db[slot]);
-      if (++c == gm.nchunk) {
-        c = 0;
-        ++b;
+    for (int64_t q = q0; q < q1; q += kBatch) {
+      double v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        v[u] = 0.0;
+        if (q + u < q1) {
+          const int64_t slot = ((b * gm.K + k) * gm.nchunk + c) * gm.D + d;
+          v[u] = src[slot * smul + sadd];
+          if (++c == gm.nchunk) {
+            c = 0;
+            ++b;
+          }
+        }
       }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (q + u < q1) s += v[u];
     }
   }
   sq[wave][lane] = s;
