@@ -43,16 +43,18 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Time-chunk length.  One chunk (no carry passes) when the (batch x
 // direction x channel-block) grid alone gives >= 4096 waves (four per SIMD
 // on the 256-CU MI355X); otherwise the sequence is cut until the main passes
-// launch ~16k waves, keeping >= 2 tiles (32 positions) per chunk.  Measured
-// on MI355X: B=32 L=196 D=3072 is fastest unchunked; B=8 L=16384 D=1536 at
-// 512-768 positions per chunk; B=2 L=196 D=1536 at 32-48.
+// launch ~16k waves, into at most ceil(tiles / 2) chunks (2 tiles = 32
+// positions each; the last may hold one).  Measured on MI355X: B=32 L=196
+// D=3072 is fastest unchunked; B=8 L=16384 D=1536 at 512-768 positions per
+// chunk; B=2 L=196 D=1536 at 32 (fwd + VJP graph replay 50.3 us, against
+// 54.8 at 48 and 60.7 at 16).
 int64_t pick_chunk_len(const mvm_scan_desc* d) {
   if (d->chunk_len > 0) return d->chunk_len;
   const int64_t tiles = ceil_div(d->seqlen, mvm::kSub);
   const int64_t waves = d->batch * d->ndir * ceil_div(d->dim, mvm::kChPerBlock) * 4;
   int64_t nchunk = 1;
   if (waves < 4096) nchunk = ceil_div(16384, std::max<int64_t>(waves, 1));
-  nchunk = std::min(nchunk, std::max<int64_t>(1, tiles / 2));
+  nchunk = std::min(nchunk, std::max<int64_t>(1, (tiles + 1) / 2));
   const int64_t tiles_per_chunk = ceil_div(tiles, nchunk);
   return std::max<int64_t>(1, tiles_per_chunk) * mvm::kSub;
 }
