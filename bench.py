@@ -48,7 +48,10 @@ captured in a HIP graph (graph_fwd_vjp_us: no host time between launches).
 
 cpu_baseline: the oracle's CPU restatement of the reference's sequential
 VisionMamba step (materialised discretisation, Python time loop, autograd)
-on this host's cores, on a bounded sample (batch 2, one step).
+on this host's cores, on a bounded sample (batch 2, one step); beside it
+the sequential and chunked scans alone at B=2, L=196, D=1536 and the
+sequential scan on a 96-channel slice of B=8, L=16384 (scaled x16 as an upper
+bound on the full width).
 """
 
 from __future__ import annotations
@@ -150,13 +153,16 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
         issued = time.perf_counter() - t0
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        return {"elapsed": elapsed, "issued": issued}, gloss
+        # the loss as a number: the tensor's autograd history would keep the
+        # capture stream's gradient-accumulation nodes alive into the eager
+        # region
+        return {"elapsed": elapsed, "issued": issued}, float(gloss.detach())
 
     mode = "graph" if graph else "eager"
     if graph:
         try:
             value_region, gloss = graph_region()
-            if not math.isfinite(float(gloss.detach())):
+            if not math.isfinite(gloss):
                 raise FloatingPointError("non-finite loss in the captured step")
         except RuntimeError as err:  # capture refused: time the eager loop
             print(f"bench.py: HIP graph capture failed ({err}); timing the eager loop",
@@ -356,7 +362,8 @@ def cpu_baseline(torch):
 def cpu_scan_baseline(torch):
     """The reference's sequential and chunked scans (restated in torch,
     materialised discretisation, per-step loop) forward + VJP on the host at
-    B=2, L=196, D=1536, N=16 fp32: 1 warm-up, median of 5."""
+    B=2, L=196, D=1536, N=16 fp32: 1 warm-up, median of 5; and the
+    sequential scan on a slice of B=8, L=16384 (cpu_long_slice)."""
     from oracle import torch_ref
     from tests import scan_inputs
     from mlx_vision_mamba_amd.scan import algorithmic_bytes
@@ -374,7 +381,34 @@ def cpu_scan_baseline(torch):
         med = sorted(times[1:])[2]
         out[name] = {"fwd_vjp_ms": round(med * 1e3, 2), "GBps": round(nbytes / med / 1e9, 3)}
     out["shape"] = "B=2 L=196 D=1536 N=16 fp32"
+    out["long_B8_L16384_slice"] = cpu_long_slice(torch)
     return out
+
+
+def cpu_long_slice(torch):
+    """The reference's sequential scan (restated in torch) forward + VJP at
+    B=8, L=16384, N=16 on an exact slice of 96 of the 1536 channels (the
+    channels are independent), fp32 arithmetic on bf16-rounded u / B / C,
+    timed once.  The full width would hold ~60 GB of materialised
+    discretisation; the slice time x 16 is reported as an upper bound on the
+    full-width time (the per-step Python and dispatch overhead does not grow
+    with the width).  The chunked restatement's VJP takes ~3x longer here
+    and is left out to bound the run."""
+    from oracle import torch_ref
+    from tests import scan_inputs
+    from mlx_vision_mamba_amd.scan import algorithmic_bytes
+    ins = [t.float() for t in scan_inputs.make(8, 16384, 96, 16, seed=4, dtype=torch.bfloat16)]
+    u, dl, A, Bm, Cm, Dv, g = ins
+    leaves = [t.clone().requires_grad_(True) for t in (u, dl, A, Bm, Cm, Dv)]
+    t0 = time.perf_counter()
+    y = torch_ref.scan_sequential(*leaves)
+    torch.autograd.grad(y, leaves, g)
+    dt = time.perf_counter() - t0
+    full = sum(algorithmic_bytes(8, 16384, 1536, 16, 2, 2))
+    return {"mode": "sequential", "slice": "B=8 L=16384 D=96 of 1536 N=16",
+            "slice_fwd_vjp_s": round(dt, 2), "scaled_fwd_vjp_s": round(16 * dt, 1),
+            "GBps_at_scaled_time": round(full / (16 * dt) / 1e9, 3),
+            "note": "scaled x16 from the slice: an upper bound on the full-width time"}
 
 
 def main():
