@@ -343,12 +343,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     constexpr bool kFull = decltype(full)::value;
     float hs[kCk + 1][4];
     float ea[kCk][4];
+    float dxs[kCk];  // delta * u of each step, reused by the reverse loop
     hs[0][0] = hin.x; hs[0][1] = hin.y; hs[0][2] = hin.z; hs[0][3] = hin.w;
 #pragma unroll
     for (int i = 0; i < kCk; ++i) {
       const int tt = h0 + i;
       const float dl = sD[buf][tt][cl];
       const float dxu = dl * sU[buf][tt][cl];
+      dxs[i] = dxu;
       const float4 b4 = *reinterpret_cast<const float4*>(&sB[buf][tt][4 * grp]);
       const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
@@ -371,7 +373,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][tt][4 * grp]);
         const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
         const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
-        const float dxu = dl * uu;
+        const float dxu = dxs[i];
         float sa = 0.f, sb = 0.f;
         float xb[4], xc[4];
 #pragma unroll
