@@ -34,6 +34,9 @@ reads for a 512 MiB copy (committed summary in profiles/, made with
 valu_busy_per_simd: the share of that kernel's cycles its SIMDs' VALU is
 issuing, rocprofv3's VALUBusy counter in the same summary (the backward is
 bound by VALU issue, so its HBM fraction follows from its instruction count).
+copy_GBps: a plain 512 MiB device-to-device copy on the same GPU, timed with
+HIP events (read + written bytes / time): the practical HBM ceiling beside
+the 8 TB/s peak.
 secondary_flops: the reference formula's work, 37 flop + 3 exp per
 (b, t, d, n) element for forward + VJP (mamba_metal_fused.py:33-145), over the
 mean fused forward + backward call time, against the 157.3 TFLOP/s fp32
@@ -180,6 +183,25 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     for kind, e0, e1, nbytes in records:
         per[kind].append((e0.elapsed_time(e1) * 1e-3, nbytes))
     return value_region, region, per, mode
+
+
+def copy_bandwidth(torch, device, iters=20):
+    """Measured HBM bandwidth of a plain 512 MiB device-to-device copy
+    (torch's copy kernel: 512 MiB read + 512 MiB written per copy), timed
+    with HIP events: the practical ceiling beside the 8 TB/s peak."""
+    n = 512 * 1024 * 1024 // 4
+    src = torch.ones(n, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    seconds = e0.elapsed_time(e1) * 1e-3 / iters
+    return round(2 * n * 4 / seconds / 1e9, 1)
 
 
 def secondary_flops(elements, seconds):
@@ -476,6 +498,8 @@ def main():
         # secondary: the reference formula's flop rate over the fused fwd +
         # VJP calls (B*K = 128 scans of L = 196, D = 768, N = 16)
         "secondary_flops": secondary_flops(32 * 4 * 196 * 768 * 16, fwd_t + bwd_t),
+        # a plain device copy on the same GPU: the practical HBM ceiling
+        "copy_GBps": copy_bandwidth(torch, device),
     }
     scans = {
         "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 200, device),
