@@ -360,7 +360,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       }
     }
     // the reverse loop reads its operands from LDS again rather than keeping
-    // the forward loop's copies live (fewer VGPRs, earlier LDS issue)
+    // the forward loop's copies live (fewer VGPRs, earlier LDS issue); only
+    // the product delta * u (dxs, one VALU per step) is kept
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = kCk - 1; i >= 0; --i) {
