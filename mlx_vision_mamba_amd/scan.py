@@ -46,6 +46,25 @@ def set_scan_timing(records):
     _timing = records
 
 
+def _timer_start():
+    """(records, start event) when launch timing is on, else (None, None).
+    The records list is read once per call, so a call that starts recording
+    also finishes it."""
+    rec = _timing
+    if rec is None:
+        return None, None
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()
+    return rec, ev
+
+
+def _timer_stop(rec, ev0, kind, nbytes_fn):
+    if rec is not None:
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev1.record()
+        rec.append((kind, ev0, ev1, nbytes_fn()))
+
+
 def algorithmic_bytes(bsz, L, D, N, in_size, out_size, ndir=1):
     """Bytes a scan forward / VJP must move if every tensor is read or
     written exactly once: (forward, vjp).  delta, ddelta, A, dA, D, dD are
@@ -170,15 +189,11 @@ def scan_forward(u, delta, A, Bm, Cm, Dv, tok=None, chunk_len=0, out_dtype=None,
                                dtype=torch.float32, device=dev)
         nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), 0))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        if _timing is not None:
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ev0.record()
+        rec, ev0 = _timer_start()
         _lib.check(lib.mvm_scan_fwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
                                     _ptr(Cm), _ptr(Dv), _ptr(y), _ptr(ckpt), _ptr(ws), nbytes,
                                     ctypes.c_void_p(_stream_ptr(dev))))
-        if _timing is not None:
-            ev1.record()
-            _timing.append(("fwd", ev0, ev1, _record("fwd", u, Bm, in_dt, out_dt)))
+        _timer_stop(rec, ev0, "fwd", lambda: _record("fwd", u, Bm, in_dt, out_dt))
     return y, ckpt
 
 
@@ -203,16 +218,12 @@ def scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt=None, tok=None, chunk_len=0,
         which = 1 if ckpt is not None else 2
         nbytes = _lib.check(lib.mvm_scan_workspace_bytes(ctypes.byref(desc), which))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        if _timing is not None:
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ev0.record()
+        rec, ev0 = _timer_start()
         _lib.check(lib.mvm_scan_bwd(ctypes.byref(desc), _ptr(u), _ptr(delta), _ptr(A), _ptr(Bm),
                                     _ptr(Cm), _ptr(Dv), _ptr(ckpt), _ptr(dy), _ptr(du),
                                     _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD),
                                     _ptr(ws), nbytes, ctypes.c_void_p(_stream_ptr(dev))))
-        if _timing is not None:
-            ev1.record()
-            _timing.append(("bwd", ev0, ev1, _record("bwd", u, Bm, in_dt, out_dt)))
+        _timer_stop(rec, ev0, "bwd", lambda: _record("bwd", u, Bm, in_dt, out_dt))
     return du, ddelta, dA, dB, dC, dD
 
 
@@ -292,19 +303,14 @@ def scan_fused_forward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, tok=None, chu
                                dtype=torch.float32, device=dev)
         nbytes = _lib.check(lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 0, int(z is not None)))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        if _timing is not None:
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ev0.record()
+        rec, ev0 = _timer_start()
         _lib.check(lib.mvm_scan_fused_fwd(
             ctypes.byref(fd), _ptr(u), _ptr(delta_raw), _ptr(delta_bias), _ptr(A), _ptr(Bm),
             _ptr(Cm), _ptr(Dv), _ptr(z), _ptr(y), _ptr(y_raw), _ptr(ckpt), _ptr(ws), nbytes,
             ctypes.c_void_p(_stream_ptr(dev))))
-        if _timing is not None:
-            ev1.record()
-            bsz, _, K, D = u.shape
-            nb = algorithmic_bytes_fused(bsz * K, L, D, A.shape[-1], K, z is not None,
-                                         delta_bias is not None)[0]
-            _timing.append(("fwd", ev0, ev1, nb))
+        _timer_stop(rec, ev0, "fwd", lambda: algorithmic_bytes_fused(
+            u.shape[0] * u.shape[2], L, u.shape[3], A.shape[-1], u.shape[2], z is not None,
+            delta_bias is not None)[0])
     return y, y_raw, ckpt
 
 
@@ -359,20 +365,15 @@ def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt,
     with torch.cuda.device(dev):
         nbytes = _lib.check(lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, int(z is not None)))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-        if _timing is not None:
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            ev0.record()
+        rec, ev0 = _timer_start()
         _lib.check(lib.mvm_scan_fused_bwd(
             ctypes.byref(fd), _ptr(u), _ptr(delta_raw), _ptr(delta_bias), _ptr(A), _ptr(Bm),
             _ptr(Cm), _ptr(Dv), _ptr(z), _ptr(y_raw), _ptr(ckpt), _ptr(dy), _ptr(du),
             _ptr(ddelta_raw), _ptr(ddelta_bias), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz),
             _ptr(ws), nbytes, ctypes.c_void_p(_stream_ptr(dev))))
-        if _timing is not None:
-            ev1.record()
-            bsz, _, K, D = u.shape
-            nb = algorithmic_bytes_fused(bsz * K, L, D, A.shape[-1], K, z is not None,
-                                         delta_bias is not None)[1]
-            _timing.append(("bwd", ev0, ev1, nb))
+        _timer_stop(rec, ev0, "bwd", lambda: algorithmic_bytes_fused(
+            u.shape[0] * u.shape[2], L, u.shape[3], A.shape[-1], u.shape[2], z is not None,
+            delta_bias is not None)[1])
     return du, ddelta_raw, ddelta_bias, dA, dB, dC, dD, dz
 
 
