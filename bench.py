@@ -3,6 +3,7 @@ scan's fwd+VJP bandwidth, printed as one JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--eager]
     python bench.py --scan-driver     (profiling driver, see scan_driver)
+    python bench.py --scan-driver-long  (profiling driver, see scan_driver_long)
 
 Workload (the step timed): VisionMamba encoder, 2D, K=4 scan directions,
 batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
@@ -332,6 +333,27 @@ def scan_driver(torch, scan, device):
           flush=True)
 
 
+def scan_driver_long(torch, scan, device):
+    """Profiling driver (--scan-driver-long): the same 512 MiB calibration
+    copy, then two plain scan forward + VJP calls at B=8, L=16384, D=1536,
+    N=16 with bf16 u / B / C / y / gradients (the long-sequence case)."""
+    from tests import scan_inputs
+    src = torch.empty(128 * 1024 * 1024, dtype=torch.float32, device=device).uniform_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    u, dl, A, Bm, Cm, Dv, g = [t.to(device) for t in scan_inputs.make(8, 16384, 1536, 16, seed=0,
+                                                                         dtype=torch.bfloat16)]
+    args = (u.unsqueeze(2), dl.unsqueeze(2), A.unsqueeze(0), Bm.unsqueeze(2), Cm.unsqueeze(2),
+            Dv.unsqueeze(0))
+    for _ in range(2):
+        y, ck = scan.scan_forward(*args, save_ckpt=True)
+        scan.scan_backward(*args, g.unsqueeze(2), ckpt=ck)
+    torch.cuda.synchronize()
+    print(json.dumps({"scan_driver": "done", "shape": "B=8 L=16384 D=1536 N=16 bf16"}), flush=True)
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")
 
 
@@ -448,6 +470,9 @@ def main():
     ap.add_argument("--scan-driver", action="store_true",
                     help="profiling driver only: a 512 MiB copy + 2 scan fwd/VJP calls at the "
                          "VisionMamba step shape")
+    ap.add_argument("--scan-driver-long", action="store_true",
+                    help="profiling driver only: a 512 MiB copy + 2 plain scan fwd/VJP calls at "
+                         "B=8 L=16384 D=1536 N=16 bf16")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the selective-scan path is benchmarked on a "
@@ -464,6 +489,9 @@ def main():
     device = torch.device("cuda:0")
     if args.scan_driver:
         scan_driver(torch, scan, device)
+        return
+    if args.scan_driver_long:
+        scan_driver_long(torch, scan, device)
         return
     if args.tune_gemms:
         gemm_tuning.start_tuning(args.tune_gemms)
