@@ -217,7 +217,7 @@ def secondary_flops(elements, seconds):
 
 
 def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
-    from tests import scan_inputs
+    from mlx_vision_mamba_amd import synthetic as scan_inputs
     u, dl, A, Bm, Cm, Dv, g = [t.to(device) for t in scan_inputs.make(bsz, L, D, N, seed=0,
                                                                          dtype=dtype)]
     args = (u.unsqueeze(2), dl.unsqueeze(2), A.unsqueeze(0), Bm.unsqueeze(2), Cm.unsqueeze(2),
@@ -337,7 +337,7 @@ def scan_driver_long(torch, scan, device):
     """Profiling driver (--scan-driver-long): the same 512 MiB calibration
     copy, then two plain scan forward + VJP calls at B=8, L=16384, D=1536,
     N=16 with bf16 u / B / C / y / gradients (the long-sequence case)."""
-    from tests import scan_inputs
+    from mlx_vision_mamba_amd import synthetic as scan_inputs
     src = torch.empty(128 * 1024 * 1024, dtype=torch.float32, device=device).uniform_()
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -409,7 +409,7 @@ def cpu_scan_baseline(torch):
     B=2, L=196, D=1536, N=16 fp32: 1 warm-up, median of 5; and the
     sequential scan on a slice of B=8, L=16384 (cpu_long_slice)."""
     from oracle import torch_ref
-    from tests import scan_inputs
+    from mlx_vision_mamba_amd import synthetic as scan_inputs
     from mlx_vision_mamba_amd.scan import algorithmic_bytes
     u, dl, A, Bm, Cm, Dv, g = scan_inputs.make(2, 196, 1536, 16, seed=0)
     nbytes = sum(algorithmic_bytes(2, 196, 1536, 16, 4, 4))
@@ -439,7 +439,7 @@ def cpu_long_slice(torch):
     with the width).  The chunked restatement's VJP takes ~3x longer here
     and is left out to bound the run."""
     from oracle import torch_ref
-    from tests import scan_inputs
+    from mlx_vision_mamba_amd import synthetic as scan_inputs
     from mlx_vision_mamba_amd.scan import algorithmic_bytes
     ins = [t.float() for t in scan_inputs.make(8, 16384, 96, 16, seed=4, dtype=torch.bfloat16)]
     u, dl, A, Bm, Cm, Dv, g = ins

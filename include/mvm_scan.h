@@ -44,6 +44,14 @@
  *   reference's (B, L, D_inner) / (B, L, N) / (D_inner, N) / (D_inner,).
  *   t is a token row; when seq_to_tok != NULL, scan position s of
  *   direction k reads and writes token row seq_to_tok[k*seqlen + s].
+ *   Outputs are written through the strides of their inputs, so every
+ *   strided layout must be non-overlapping (ordered by stride, each stride
+ *   at least the span of the smaller dimensions; a stride-0 broadcast over
+ *   a dimension of size > 1 is rejected with MVM_ERR_INVALID_ARG).
+ *   Each row of seq_to_tok must be a permutation of 0..seqlen-1: the kernels
+ *   only clamp entries into [0, seqlen), so a row that misses a token leaves
+ *   that token's outputs unwritten and a repeated token is written twice
+ *   (the table lives in device memory and is not inspected on the host).
  */
 #ifndef MVM_SCAN_H
 #define MVM_SCAN_H

@@ -10,6 +10,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
+#include <utility>
 
 #include "conv_kernels.h"
 #include "mvm_conv.h"
@@ -59,6 +61,27 @@ int64_t pick_chunk_len(const mvm_scan_desc* d) {
   return std::max<int64_t>(1, tiles_per_chunk) * mvm::kSub;
 }
 
+// True when a strided layout maps no two index tuples to one element:
+// ordered by stride, every dimension's stride clears the span of the
+// smaller ones (dimensions of size <= 1 are skipped).  Outputs are written
+// through the same strides as their inputs, so an overlapping layout would
+// make writes race.  A layout with no elements cannot overlap.
+bool no_overlap(std::initializer_list<std::pair<int64_t, int64_t>> dims) {  // (size, stride)
+  std::pair<int64_t, int64_t> v[8];
+  int n = 0;
+  for (const auto& d : dims) {
+    if (d.first == 0) return true;
+    if (d.first > 1 && n < 8) v[n++] = {d.second, d.first};  // (stride, size)
+  }
+  std::sort(v, v + n);
+  int64_t span = 1;
+  for (int i = 0; i < n; ++i) {
+    if (v[i].first < span) return false;
+    span = v[i].first * v[i].second;
+  }
+  return true;
+}
+
 int check_desc(const mvm_scan_desc* d) {
   if (d == nullptr) return fail(MVM_ERR_INVALID_ARG, "desc is NULL");
   if (d->batch < 0 || d->seqlen < 0 || d->dim < 0)
@@ -79,12 +102,18 @@ int check_desc(const mvm_scan_desc* d) {
                               d->bc_stride_b, d->bc_stride_k, d->bc_stride_t};
   for (int64_t s : strides)
     if (s < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride");
-  if (d->seqlen > 1 && d->x_stride_t < d->dim)
-    return fail(MVM_ERR_INVALID_ARG, "x_stride_t=%lld overlaps channels (dim=%lld)",
-                (long long)d->x_stride_t, (long long)d->dim);
-  if (d->seqlen > 1 && d->bc_stride_t < d->dstate)
-    return fail(MVM_ERR_INVALID_ARG, "bc_stride_t=%lld overlaps states (dstate=%lld)",
-                (long long)d->bc_stride_t, (long long)d->dstate);
+  if (!no_overlap({{d->batch, d->x_stride_b}, {d->ndir, d->x_stride_k}, {d->seqlen, d->x_stride_t},
+                   {d->dim, 1}}))
+    return fail(MVM_ERR_INVALID_ARG,
+                "x strides (b=%lld k=%lld t=%lld) overlap for batch=%lld ndir=%lld seqlen=%lld dim=%lld",
+                (long long)d->x_stride_b, (long long)d->x_stride_k, (long long)d->x_stride_t,
+                (long long)d->batch, (long long)d->ndir, (long long)d->seqlen, (long long)d->dim);
+  if (!no_overlap({{d->batch, d->bc_stride_b}, {d->ndir, d->bc_stride_k}, {d->seqlen, d->bc_stride_t},
+                   {d->dstate, 1}}))
+    return fail(MVM_ERR_INVALID_ARG,
+                "bc strides (b=%lld k=%lld t=%lld) overlap for batch=%lld ndir=%lld seqlen=%lld dstate=%lld",
+                (long long)d->bc_stride_b, (long long)d->bc_stride_k, (long long)d->bc_stride_t,
+                (long long)d->batch, (long long)d->ndir, (long long)d->seqlen, (long long)d->dstate);
   if (d->batch * d->ndir > 65535)
     return fail(MVM_ERR_UNSUPPORTED, "batch*ndir=%lld exceeds 65535",
                 (long long)(d->batch * d->ndir));
@@ -312,14 +341,24 @@ int check_fused(const mvm_scan_fused_desc* fd) {
                          fd->z_stride_b, fd->z_stride_k, fd->z_stride_t};
   for (int64_t v : st)
     if (v < 0) return fail(MVM_ERR_INVALID_ARG, "negative stride in fused desc");
-  const int64_t dim = fd->scan.dim;
-  if (fd->scan.seqlen > 1 &&
-      (fd->dt_stride_t < dim || fd->y_stride_t < dim || (fd->z_stride_t != 0 && fd->z_stride_t < dim)))
-    return fail(MVM_ERR_INVALID_ARG, "fused row stride overlaps channels (dim=%lld)", (long long)dim);
+  const mvm_scan_desc& sd = fd->scan;
+  if (!no_overlap({{sd.batch, fd->dt_stride_b}, {sd.ndir, fd->dt_stride_k}, {sd.seqlen, fd->dt_stride_t},
+                   {sd.dim, 1}}) ||
+      !no_overlap({{sd.batch, fd->y_stride_b}, {sd.ndir, fd->y_stride_k}, {sd.seqlen, fd->y_stride_t},
+                   {sd.dim, 1}}))
+    return fail(MVM_ERR_INVALID_ARG, "fused desc: delta_raw or y strides overlap (dim=%lld)",
+                (long long)sd.dim);
   if (fd->scan.batch * fd->scan.ndir * fd->scan.seqlen > INT32_MAX)
     return fail(MVM_ERR_UNSUPPORTED, "batch*ndir*seqlen exceeds 2^31-1");
   if (fd->reserved != 0) return fail(MVM_ERR_INVALID_ARG, "fused desc: reserved must be 0");
   return MVM_OK;
+}
+
+// z / dz strides (checked only when a gate is given: without one they are 0)
+bool z_ok(const mvm_scan_fused_desc* fd) {
+  const mvm_scan_desc& sd = fd->scan;
+  return no_overlap({{sd.batch, fd->z_stride_b}, {sd.ndir, fd->z_stride_k}, {sd.seqlen, fd->z_stride_t},
+                     {sd.dim, 1}});
 }
 
 mvm::Geom fused_geom(const mvm_scan_fused_desc* fd) {
@@ -383,6 +422,7 @@ int mvm_scan_fused_fwd(const mvm_scan_fused_desc* desc, const float* u, const fl
   if (!empty) {
     if (!u || !delta_raw || !A || !Bm || !Cm || !Dv || !y)
       return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_fwd: NULL input or y pointer");
+    if (z && !z_ok(desc)) return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_fwd: z strides overlap");
     if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
       return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_fwd: ckpt must be 16-byte aligned");
   }
@@ -420,6 +460,7 @@ int mvm_scan_fused_bwd(const mvm_scan_fused_desc* desc, const float* u, const fl
       return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: NULL output pointer");
     if (gate && (!y_raw || !dz))
       return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: a gate needs y_raw and dz");
+    if (gate && !z_ok(desc)) return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: z strides overlap");
     if ((reinterpret_cast<uintptr_t>(ckpt) & 15u) != 0)
       return fail(MVM_ERR_INVALID_ARG, "mvm_scan_fused_bwd: ckpt must be 16-byte aligned");
   }

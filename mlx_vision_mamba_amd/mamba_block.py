@@ -43,9 +43,10 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import directions as _dirs
-from .conv import conv_silu_backward_into, conv_silu_forward_into
+from .conv import causal_conv_silu, conv_silu_backward_into, conv_silu_forward_into
 from .norm import layer_norm
-from .scan import get_scan_fn, mode_chunk_len, scan_fused_backward, scan_fused_forward
+from .scan import (check_permutation_table, get_scan_fn, mode_chunk_len, scan_fused_backward,
+                   scan_fused_forward)
 
 
 def _dt_bias_init(d_inner: int, dt_min: float = 1e-3, dt_max: float = 1e-1) -> torch.Tensor:
@@ -61,6 +62,13 @@ class MambaBlock(nn.Module):
     scan_mode: "sequential", "chunked", "parallel", "metal", "metal_train",
     "metal_fused" (the reference's names, mamba_block.py:104-120) or "hip";
     every mode runs the HIP scan.  Unknown names raise ValueError.
+
+    ``self._scan_fn`` is the scan function the mode selects
+    (mamba_block.py:104-122).  The library's modes run inside the fused
+    block core; a caller that assigns another callable
+    ``f(x, delta, A, B, C, D) -> y`` to ``_scan_fn`` gets the reference's op
+    sequence with ``f`` called where the reference calls it (:187), in this
+    block and in the direction blocks that contain it.
     """
 
     def __init__(self, d_model: int = 384, d_state: int = 16, d_conv: int = 4,
@@ -86,6 +94,8 @@ class MambaBlock(nn.Module):
         self.out_proj = nn.Linear(self.d_inner, d_model, bias=False)           # :153
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _custom_scan(self):
+            return _scan_fn_forward(self, x)
         return _directional_forward([self], x, None, self.scan_mode)
 
 
@@ -120,6 +130,8 @@ class BidirectionalMambaBlock(nn.Module):
         h, xr = layer_norm(x, self.norm, residual=True)                      # :227
         tok = _cached_table(self._tables, 2, x.shape[1], None, x.device)
         blocks = [self.forward_mamba, self.backward_mamba]
+        if any(_custom_scan(b) for b in blocks):
+            return xr + _per_direction_forward(blocks, h, tok)
         return xr + _directional_forward(blocks, h, tok, self.scan_mode,
                                          _direction_stacks(self, blocks))
 
@@ -155,7 +167,6 @@ class MultiDirectionalMambaBlock(nn.Module):
         bsz, n, _ = x.shape
         h, xr = layer_norm(x, self.norm, residual=True)                      # :548
         expected = math.prod(self.grid_shape) if self.grid_shape is not None else n
-        stacks = _direction_stacks(self, list(self.mamba_blocks))
         if n != expected and self.num_directions > 2:                         # :554-559
             tok = _cached_table(self._tables, 2, n, None, x.device)
             blocks = [self.mamba_blocks[0], self.mamba_blocks[1]]
@@ -163,6 +174,9 @@ class MultiDirectionalMambaBlock(nn.Module):
             grid = self.grid_shape if self.num_directions > 2 else None
             tok = _cached_table(self._tables, self.num_directions, n, grid, x.device)
             blocks = list(self.mamba_blocks)
+        if any(_custom_scan(b) for b in blocks):
+            return xr + _per_direction_forward(blocks, h, tok)
+        stacks = _direction_stacks(self, list(self.mamba_blocks))
         return xr + _directional_forward(blocks, h, tok, self.scan_mode, stacks)  # :562-566
 
 
@@ -253,7 +267,9 @@ class _DirectionParams(torch.autograd.Function):
 def _cached_table(cache, K, n, grid, device):
     key = (K, n, grid, str(device))
     if key not in cache:
-        cache[key] = _dirs.seq_to_tok_table(K, n, grid).to(device)
+        table = _dirs.seq_to_tok_table(K, n, grid).to(device)
+        check_permutation_table(table)
+        cache[key] = table
     return cache[key]
 
 
@@ -276,7 +292,7 @@ class _MambaCoreFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, tok, chunk_len, detach):
+    def forward(ctx, xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv, tok, chunk_len, save):
         bsz, n, K, d2 = xz.shape
         din = d2 // 2
         R = W_dt.shape[2]
@@ -290,7 +306,8 @@ class _MambaCoreFn(torch.autograd.Function):
         dt = dbc[..., :R]
         delta_raw = torch.bmm(dt, W_dt.transpose(1, 2))                            # :180
         bc = _bnkd(dbc, bsz, n)
-        save = not detach
+        # save: checkpoints and y_raw are kept for the backward (training);
+        # off for the forward-only mode and under no_grad / inference_mode
         y, y_raw, ckpt = scan_fused_forward(_bnkd(xc, bsz, n), _bnkd(delta_raw, bsz, n), b_dt, A_log,
                                             bc[..., R:R + ns], bc[..., R + ns:], Dv, z, tok,
                                             chunk_len, save=save, a_is_log=True)   # :181-190
@@ -348,6 +365,47 @@ def _tn_split_rows(a, b, splits=8):
     return part.view(K, splits, P, -1).sum(1)
 
 
+def _custom_scan(blk):
+    """True when the caller replaced ``blk._scan_fn`` with a function other
+    than the one its ``scan_mode`` selects (mamba_block.py:104-122).  The
+    library's own modes all compute the same scan, which the fused block
+    core runs; any other callable is honoured by _scan_fn_forward."""
+    return blk._scan_fn is not get_scan_fn(blk.scan_mode)
+
+
+def _scan_fn_forward(blk, x):
+    """MambaBlock.__call__ in the reference's op sequence
+    (mamba_block.py:155-192), calling ``blk._scan_fn(x, delta, A, B, C, D)``
+    at :187.  Used when a block's scan function was replaced; the conv +
+    SiLU runs on the HIP conv kernel, the rest on torch ops."""
+    din, ns, R = blk.d_inner, blk.d_state, blk.dt_rank
+    xz = F.linear(x, blk.in_proj.weight)                                      # :165
+    xb, z = xz[..., :din], xz[..., din:]                                       # :166-167
+    conv_w = blk.conv1d.weight.reshape(1, din, blk.d_conv)
+    xc = causal_conv_silu(xb.unsqueeze(2), conv_w, blk.conv1d.bias.unsqueeze(0)).squeeze(2)  # :170-171
+    dbc = F.linear(xc, blk.x_proj.weight)                                      # :174
+    dt, Bm, Cm = dbc[..., :R], dbc[..., R:R + ns], dbc[..., R + ns:]           # :175-177
+    delta = F.softplus(F.linear(dt, blk.dt_proj.weight, blk.dt_proj.bias))     # :180-181
+    A = -torch.exp(blk.A_log)                                                  # :184
+    y = blk._scan_fn(xc, delta, A, Bm, Cm, blk.D)                              # :187
+    y = y * F.silu(z)                                                          # :190
+    return F.linear(y, blk.out_proj.weight)                                    # :191
+
+
+def _per_direction_forward(blocks, h, tok):
+    """Sum over directions of block k run on h in the scan order tok[k]
+    (a gathered copy, as the reference builds, mamba_block.py:407-533), its
+    output put back in token order.  Used when a block's scan function was
+    replaced, so that each block's own ``__call__`` runs."""
+    y = None
+    for k, blk in enumerate(blocks):
+        order = tok[k].long()
+        out = blk(h[:, order])
+        out = out[:, torch.argsort(order)]
+        y = out if y is None else y + out
+    return y
+
+
 def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
     """Run len(blocks) MambaBlocks on one (B, N, E) input, block k scanning
     in the order of tok[k], and return the sum of their outputs.  ``stacks``:
@@ -374,7 +432,8 @@ def _directional_forward(blocks, h, tok, scan_mode, stacks=None):
     args = [t.float() for t in (xz, conv_w, conv_b, W_x, W_dt, b_dt, A_log, Dv)]
     if detach:
         args = [t.detach() for t in args]
-    y = _MambaCoreFn.apply(*args, tok, mode_chunk_len(scan_mode), detach)     # :170-190
+    save = not detach and torch.is_grad_enabled() and any(t.requires_grad for t in args)
+    y = _MambaCoreFn.apply(*args, tok, mode_chunk_len(scan_mode), save)       # :170-190
     # (K, E, Din) -> (E, K*Din): the out_proj of the concatenated directions
     # is their (atomic-free) sum
     W_out = W_out.permute(1, 0, 2).reshape(W_out.shape[1], K * din)

@@ -161,7 +161,11 @@ def _prepare(u, delta, A, Bm, Cm, Dv):
     u = u.to(in_dt).contiguous()
     Bm = Bm.to(in_dt)
     Cm = Cm.to(in_dt)
-    if not (Bm.stride() == Cm.stride() and Bm.stride(-1) == 1 and min(Bm.stride()) >= 0):
+    # B / C views (e.g. column slices of a projection output) are kept when
+    # they share strides and no two elements overlap; a broadcast (stride 0)
+    # layout is copied, so that dB / dC get one element per (b, t, k, n)
+    if not (Bm.stride() == Cm.stride() and Bm.stride(-1) == 1 and min(Bm.stride()) >= 0
+            and _no_overlap(Bm)):
         Bm, Cm = Bm.contiguous(), Cm.contiguous()
     delta = delta.to(torch.float32).contiguous()
     A = A.to(torch.float32).contiguous()
@@ -348,12 +352,14 @@ def scan_fused_backward(u, delta_raw, delta_bias, A, Bm, Cm, Dv, z, y_raw, ckpt,
     du = like(u) if du is None else du
     ddelta_raw = like(delta_raw) if ddelta_raw is None else ddelta_raw
     if dB is None or dC is None:
-        dB = torch.empty_strided(Bm.shape, Bm.stride(), dtype=torch.float32, device=dev)
-        dC = torch.empty_strided(Bm.shape, Bm.stride(), dtype=torch.float32, device=dev)
+        dB, dC = like(Bm), like(Bm)
     if dB.stride() != Bm.stride() or dC.stride() != Bm.stride():
         raise ValueError("dB and dC must have the strides of B")
     if z is not None and dz is None:
         dz = like(z)
+    for t in (du, ddelta_raw, dB, dC) + ((dz,) if z is not None else ()):
+        if not _no_overlap(t):
+            raise ValueError("gradient views must not overlap themselves")
     if (z is not None and dz.stride() != z.stride()) or ddelta_raw.stride() != delta_raw.stride() \
             or du.stride() != u.stride():
         raise ValueError("gradient views must have the strides of their primals")
@@ -382,8 +388,10 @@ class _SelectiveScanFn(torch.autograd.Function):
     (the custom_function + vjp pair of mamba_metal_fused.py:229-250)."""
 
     @staticmethod
-    def forward(ctx, u, delta, A, Bm, Cm, Dv, tok, chunk_len, out_dtype):
-        needs = any(ctx.needs_input_grad[:6])
+    def forward(ctx, u, delta, A, Bm, Cm, Dv, tok, chunk_len, out_dtype, grad_mode):
+        # checkpoints only when a gradient can be asked for; grad mode is off
+        # inside forward, so the caller passes its own (grad_mode)
+        needs = grad_mode and any(ctx.needs_input_grad[:6])
         y, ckpt = scan_forward(u, delta, A, Bm, Cm, Dv, tok, chunk_len, out_dtype, save_ckpt=needs)
         ctx.chunk_len = chunk_len
         ctx.out_dtype = out_dtype
@@ -397,7 +405,26 @@ class _SelectiveScanFn(torch.autograd.Function):
         u, delta, A, Bm, Cm, Dv, ckpt, tok = ctx.saved_tensors
         grads = scan_backward(u, delta, A, Bm, Cm, Dv, dy, ckpt, tok, ctx.chunk_len, ctx.out_dtype)
         grads = tuple(g.to(dt) for g, dt in zip(grads, ctx.in_dtypes))
-        return grads + (None, None, None)
+        return grads + (None, None, None, None)
+
+
+def check_permutation_table(table):
+    """Raises ValueError unless every row of the (K, L) table is a
+    permutation of 0..L-1.  The kernels only clamp table entries into
+    [0, L): a row that misses a token would leave that token's outputs
+    unwritten and a repeated token would be written twice.  The check runs
+    once per table tensor (and again after an in-place change)."""
+    stamp = (table.data_ptr(), table._version)
+    if getattr(table, "_mvm_perm_checked", None) == stamp:
+        return
+    K, L = table.shape
+    ok = True
+    if L > 0:
+        srt = torch.sort(table.long(), dim=1).values
+        ok = bool((srt == torch.arange(L, device=table.device)).all())
+    if not ok:
+        raise ValueError("seq_to_tok: every row must be a permutation of 0..L-1")
+    table._mvm_perm_checked = stamp
 
 
 def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0, out_dtype=None,
@@ -414,18 +441,26 @@ def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0
         if seq_to_tok.dtype != torch.int32 or seq_to_tok.shape != (u.shape[2], u.shape[1]):
             raise ValueError("seq_to_tok must be int32 of shape (K, L)")
         seq_to_tok = seq_to_tok.to(u.device).contiguous()
+        check_permutation_table(seq_to_tok)
     if forward_only:
         y, _ = scan_forward(u.detach(), delta.detach(), A.detach(), B.detach(), C.detach(),
                             D.detach(), seq_to_tok, _resolve_chunk(u.shape[1], chunk_len), out_dtype)
         return y
-    return _SelectiveScanFn.apply(u, delta, A, B, C, D, seq_to_tok, chunk_len, out_dtype)
+    return _apply_scan(u, delta, A, B, C, D, seq_to_tok, chunk_len, out_dtype)
+
+
+def _apply_scan(u, delta, A, B, C, D, tok, chunk_len, out_dtype):
+    """_SelectiveScanFn.apply, saving checkpoints only when grad mode is on
+    (not under torch.no_grad / inference_mode)."""
+    return _SelectiveScanFn.apply(u, delta, A, B, C, D, tok, chunk_len, out_dtype,
+                                  torch.is_grad_enabled())
 
 
 def _scan3(x, delta, A, B, C, D, chunk_len, out_dtype=None):
     if x.dim() != 3:
         raise ValueError(f"x must be (B, L, D); got {tuple(x.shape)}")
-    y = _SelectiveScanFn.apply(x.unsqueeze(2), delta.unsqueeze(2), A.unsqueeze(0), B.unsqueeze(2),
-                               C.unsqueeze(2), D.unsqueeze(0), None, chunk_len, out_dtype)
+    y = _apply_scan(x.unsqueeze(2), delta.unsqueeze(2), A.unsqueeze(0), B.unsqueeze(2),
+                    C.unsqueeze(2), D.unsqueeze(0), None, chunk_len, out_dtype)
     return y.squeeze(2)
 
 

@@ -1,4 +1,5 @@
-"""Seeded synthetic scan inputs shared by tests and bench.py.
+"""Seeded synthetic selective-scan inputs (the benchmark workloads' recipe),
+used by bench.py and the tests.
 
 Recipe (generated in this order on a CPU torch.Generator):
 u ~ N(0,1) (B,L,D); delta = softplus(0.5*N(0,1) - 4.6) (B,L,D), i.e. dt in

@@ -21,9 +21,30 @@ Pinning (each function is checked by something other than a retyped formula):
                       epilogue around the scan) torch float64 autograd through
                       ``F.softplus`` / ``F.silu`` and the independent torch
                       scan restatement; tests/test_oracle.py.
+* ``direction_axis_order`` / ``seq_to_token``  the materialised torch
+                      reshape / permute / flip of the reference's helpers and
+                      a hand-derived K=6 case; tests/test_oracle.py.
 
-No golden vectors exist in the reference (it has no tests); the fixtures under
-tests/golden/ are written by this oracle after the checks above pass.
+The other oracle pieces are pinned in the same way:
+
+* scan_ref.c ``oracle_scan_fwd`` / ``oracle_scan_vjp``: equal to this module
+  (tests/test_oracle.py::test_c_oracle_matches_numpy).
+* scan_ref.c ``oracle_ddelta_scale`` (the cancellation scale S that widens
+  the ddelta bound): S >= |ddelta| everywhere, S = |ddelta| exactly on
+  inputs whose terms share one sign (both terms exercised), the delta = 0
+  closed form over a reverse cumsum, and homogeneity in g and u.
+* torch_ref ``scan_sequential`` / ``scan_chunked``: autograd and
+  ``gradcheck`` (tests/test_oracle.py); ``mamba_block``, ``layer_norm``,
+  ``direction_block``, ``bidirectional_block``, ``vision_mamba``: closed
+  forms from ``np.convolve`` / ``np.cumsum`` at unit decay, a hand-written
+  two-token scan with decay, a textbook LayerNorm, numpy-built scan orders
+  and a brute-force patch embedding, each shown sensitive to the plausible
+  mistakes (tests/test_oracle_blocks.py).
+
+No golden vectors exist in the reference (it has no tests).  The fixtures
+under tests/golden/ are written from this oracle (and scan_ref.c) by
+tests/golden/make_golden.py after the checks above pass; tests/test_golden.py
+checks that the oracle still reproduces them.
 """
 
 from __future__ import annotations

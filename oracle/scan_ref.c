@@ -148,7 +148,9 @@ int oracle_scan_vjp(int64_t Bsz, int64_t L, int64_t D, int64_t N,
  * + |B_n u_t|), the sum of the absolute values of the terms whose signed sum
  * is ddelta (same adjoint recurrence as oracle_scan_vjp).  An fp32
  * evaluation of ddelta cannot be closer than about 2^-24 * S to the exact
- * value, so the GPU parity test widens its bound by a multiple of S. */
+ * value, so the GPU parity test widens its bound by a multiple of S.
+ * Pinned in tests/test_oracle.py: S >= |ddelta|; S == |ddelta| when every
+ * term has one sign; the delta = 0 closed form; homogeneity in g and u. */
 int oracle_ddelta_scale(int64_t Bsz, int64_t L, int64_t D, int64_t N,
                         const float* u, const float* delta, const float* A,
                         const float* Bm, const float* Cm, const float* g,

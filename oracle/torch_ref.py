@@ -18,6 +18,7 @@ Two uses:
    product's modules by name and apply the reference's materialised
    permutations (reshape / transpose / flip), so that the product's
    index-remapped path is checked against the reference's formulation.
+   They are pinned by closed forms in tests/test_oracle_blocks.py.
 """
 
 from __future__ import annotations

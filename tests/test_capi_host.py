@@ -90,12 +90,36 @@ def test_valid_desc_and_sizes():
     ("x_stride_t", 3, _lib.MVM_ERR_INVALID_ARG),
     ("bc_stride_t", 2, _lib.MVM_ERR_INVALID_ARG),
     ("x_stride_b", -5, _lib.MVM_ERR_INVALID_ARG),
+    ("x_stride_b", 0, _lib.MVM_ERR_INVALID_ARG),    # batch 2 broadcast: du would race
+    ("bc_stride_b", 0, _lib.MVM_ERR_INVALID_ARG),
+    ("x_stride_b", 24 * 39, _lib.MVM_ERR_INVALID_ARG),  # batch 1 overlaps batch 0's last row
 ])
 def test_bad_descriptors_rejected(field, value, code):
     d = _desc()
     setattr(d, field, value)
     assert _validate(d) == code
     assert _lib.last_error() != ""
+
+
+@pytest.mark.parametrize("field", ["x_stride_k", "bc_stride_k"])
+def test_direction_stride_zero_rejected_with_several_directions(field):
+    d = _desc(K=2)
+    assert _validate(d) == 0
+    setattr(d, field, 0)
+    assert _validate(d) == _lib.MVM_ERR_INVALID_ARG
+    assert "overlap" in _lib.last_error()
+
+
+def test_size_one_dimensions_take_any_stride():
+    """A dimension of size 1 is never stepped, so its stride is free."""
+    d = _desc(B=1, K=1)
+    d.x_stride_b = d.bc_stride_b = 0
+    d.x_stride_k = d.bc_stride_k = 0
+    assert _validate(d) == 0
+    # interleaved layouts that do not overlap pass: (b, t) strides (24, 48)
+    d = _desc(B=2, L=40, D=24)
+    d.x_stride_b, d.x_stride_t = 24, 48
+    assert _validate(d) == 0
 
 
 def test_null_pointers_rejected_before_launch():
@@ -220,7 +244,7 @@ def _fdesc(B=2, L=40, D=24, N=16, K=3):
 
 @pytest.mark.parametrize("field,value,code", [
     ("dt_stride_t", 3, _lib.MVM_ERR_INVALID_ARG), ("y_stride_b", -1, _lib.MVM_ERR_INVALID_ARG),
-    ("z_stride_t", 5, _lib.MVM_ERR_INVALID_ARG),
+    ("y_stride_b", 0, _lib.MVM_ERR_INVALID_ARG), ("dt_stride_k", 0, _lib.MVM_ERR_INVALID_ARG),
 ])
 def test_fused_bad_descriptors_rejected(field, value, code):
     lib = _lib.lib()
@@ -347,3 +371,20 @@ def test_norm_workspace_and_host_checks():
     assert lib.mvm_layernorm_bwd(ctypes.byref(d), *([fake] * 10), need - 1, null) == _lib.MVM_ERR_WORKSPACE
     assert lib.mvm_layernorm_bwd(ctypes.byref(d), fake, fake, fake, fake, fake, null, fake, null, fake,
                                  fake, need, null) == _lib.MVM_ERR_INVALID_ARG
+
+
+def test_fused_overlapping_gate_rejected_before_launch():
+    """z strides are checked when a gate is given (without one they are 0);
+    an overlapping z / dz layout fails before anything is launched."""
+    lib = _lib.lib()
+    fd = _fdesc()
+    fd.z_stride_t = 5
+    assert lib.mvm_scan_fused_validate(ctypes.byref(fd)) == 0
+    fake, null = ctypes.c_void_p(0x1000), ctypes.c_void_p(0)
+    need = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 0, 1)
+    ws = ctypes.c_void_p(0x100000)
+    rc = lib.mvm_scan_fused_fwd(ctypes.byref(fd), *([fake] * 10), null, ws, need, null)
+    assert rc == _lib.MVM_ERR_INVALID_ARG and "z strides" in _lib.last_error()
+    need = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1)
+    rc = lib.mvm_scan_fused_bwd(ctypes.byref(fd), *([fake] * 19), ws, need, null)
+    assert rc == _lib.MVM_ERR_INVALID_ARG and "z strides" in _lib.last_error()

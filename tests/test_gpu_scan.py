@@ -18,7 +18,7 @@ import pytest
 import torch
 
 from oracle import ref_lib, scan_oracle as so
-from tests import scan_inputs
+from mlx_vision_mamba_amd import synthetic as scan_inputs
 
 pytestmark = pytest.mark.gpu
 

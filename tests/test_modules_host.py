@@ -135,3 +135,22 @@ def test_direction_params_route_gradients_to_slices(K_used):
                 assert torch.equal(g, w[k]), (name, k)
             else:
                 assert g is None, (name, k)
+
+
+def test_permutation_check_on_host_tables():
+    from mlx_vision_mamba_amd import scan
+    t = dirs.seq_to_tok_table(4, 12, (3, 4))
+    scan.check_permutation_table(t)
+    assert t._mvm_perm_checked == (t.data_ptr(), t._version)
+    bad = t.clone()
+    bad[2, 0] = bad[2, 1]
+    with pytest.raises(ValueError, match="permutation"):
+        scan.check_permutation_table(bad)
+    scan.check_permutation_table(torch.zeros(3, 0, dtype=torch.int32))
+
+
+def test_replaced_scan_fn_is_detected():
+    blk = mb.MambaBlock(16, scan_mode="chunked")
+    assert not mb._custom_scan(blk)
+    blk._scan_fn = lambda *a: a[0]
+    assert mb._custom_scan(blk)
