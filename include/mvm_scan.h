@@ -135,6 +135,36 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Backward without a workspace.  No counterpart in the reference: this is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same as mvm_scan_bwd with a caller checkpoint, but the scratch space
+ * (chunk aggregates, dA / dD and dB / dC partial sums) comes from a fixed
+ * device array of MVM_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * GPU it runs on until the process ends; it calls no hipMalloc / hipFree.
+ *   - ckpt is required (NULL fails with MVM_ERR_INVALID_ARG).
+ *   - A shape whose scratch need, mvm_scan_workspace_bytes(desc, 1),
+ *     exceeds MVM_NOALLOC_SCRATCH_BYTES fails with MVM_ERR_WORKSPACE before
+ *     anything is launched (B=2 L=196 D=1536 needs ~5.6 MB; B*K=128 L=196
+ *     D=768 needs ~52 MB).
+ *   - All calls on one GPU share its array: calls that overlap in time on
+ *     one GPU (other streams, other threads) race.  Calls in order on one
+ *     stream are safe.  Nothing in the array needs clearing: every element
+ *     the kernels read is written earlier in the same call.
+ * ---------------------------------------------------------------------- */
+#define MVM_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)
+
+/* MVM_NOALLOC_SCRATCH_BYTES, as compiled into the loaded library. */
+int64_t mvm_scan_noalloc_scratch_bytes(void);
+
+int mvm_scan_bwd_noalloc(const mvm_scan_desc* desc, const void* u, const float* delta,
+                         const float* A, const void* Bm, const void* Cm,
+                         const float* Dv, const float* ckpt, const void* dy, void* du,
+                         float* ddelta, float* dA, void* dB, void* dC, float* dD,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused form: the Mamba block's prologue and epilogue around the scan.
  *
  * Replaces, for one block call, the ops around scan_fn in MambaBlock

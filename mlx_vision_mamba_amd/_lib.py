@@ -89,6 +89,8 @@ SIGNATURES = {
     "mvm_scan_chunk_len": (_i64, [ctypes.POINTER(ScanDesc)]),
     "mvm_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 9 + [ctypes.c_size_t, _vp]),
     "mvm_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 15 + [ctypes.c_size_t, _vp]),
+    "mvm_scan_noalloc_scratch_bytes": (_i64, []),
+    "mvm_scan_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(ScanDesc)] + [_vp] * 15),
     "mvm_scan_fused_validate": (ctypes.c_int, [ctypes.POINTER(FusedDesc)]),
     "mvm_scan_fused_workspace_bytes": (_i64, [ctypes.POINTER(FusedDesc), ctypes.c_int, ctypes.c_int]),
     "mvm_scan_fused_fwd": (ctypes.c_int, [ctypes.POINTER(FusedDesc)] + [_vp] * 12 + [ctypes.c_size_t, _vp]),

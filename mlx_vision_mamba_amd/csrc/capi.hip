@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <utility>
 
 #include "conv_kernels.h"
@@ -322,6 +323,86 @@ int mvm_scan_bwd(const mvm_scan_desc* desc, const void* u, const float* delta, c
   mvm::BwdBufs b{u, delta, A, Bm, Cm, Dv, ckpt, dy, du, ddelta, dA, dB, dC, dD,
                  agg_mu, agg_s, part_dA, part_dD, part_bc};
   return hip_status(mvm::launch_bwd(g, b, desc->in_dtype, desc->out_dtype, s), "mvm_scan_bwd launch");
+}
+
+}  // extern "C"
+
+// ------------------------------------------- backward without a workspace
+
+namespace {
+
+// Scratch of mvm_scan_bwd_noalloc: one array per GPU (each device that loads
+// the library holds its own copy until the process ends).  Host code never
+// uses the name `scratch` as an address: it is a host-side stand-in for the
+// symbol, and the device address comes from hipGetSymbolAddress, once per
+// device with that device current.
+constexpr size_t kNoallocBytes = MVM_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the scratch array of the GPU `stream` runs on (the
+// current device for the null stream).
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "mvm_scan_bwd_noalloc: device of the stream");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MVM_ERR_UNSUPPORTED, "mvm_scan_bwd_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return hip_status(e, "mvm_scan_bwd_noalloc: hipGetSymbolAddress(scratch)");
+    if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & (kAlign - 1)) != 0)
+      return fail(MVM_ERR_HIP, "mvm_scan_bwd_noalloc: scratch address %p is not %zu-byte aligned", p,
+                  kAlign);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MVM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t mvm_scan_noalloc_scratch_bytes(void) { return static_cast<int64_t>(kNoallocBytes); }
+
+int mvm_scan_bwd_noalloc(const mvm_scan_desc* desc, const void* u, const float* delta,
+                         const float* A, const void* Bm, const void* Cm, const float* Dv,
+                         const float* ckpt, const void* dy, void* du, float* ddelta, float* dA,
+                         void* dB, void* dC, float* dD, void* stream) {
+  int rc = check_desc(desc);
+  if (rc != MVM_OK) return rc;
+  const mvm::Geom g = make_geom(desc);
+  const bool empty = g.B == 0 || g.L == 0 || g.D == 0;
+  if (empty)  // only dA / dD are owed (zero fills): no scratch
+    return mvm_scan_bwd(desc, u, delta, A, Bm, Cm, Dv, ckpt, dy, du, ddelta, dA, dB, dC, dD, nullptr,
+                        0, stream);
+  if (ckpt == nullptr)
+    return fail(MVM_ERR_INVALID_ARG,
+                "mvm_scan_bwd_noalloc: ckpt is required (recomputing it needs checkpoint-sized scratch)");
+  const size_t need = bwd_ws(g, false).total;
+  if (need > kNoallocBytes)
+    return fail(MVM_ERR_WORKSPACE,
+                "mvm_scan_bwd_noalloc: this shape needs %zu bytes of scratch, more than the %zu-byte "
+                "static array; call mvm_scan_bwd with a workspace",
+                need, kNoallocBytes);
+  void* ws = nullptr;
+  rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws);
+  if (rc != MVM_OK) return rc;
+  return mvm_scan_bwd(desc, u, delta, A, Bm, Cm, Dv, ckpt, dy, du, ddelta, dA, dB, dC, dD, ws,
+                      kNoallocBytes, stream);
 }
 
 }  // extern "C"

@@ -388,3 +388,24 @@ def test_fused_overlapping_gate_rejected_before_launch():
     need = lib.mvm_scan_fused_workspace_bytes(ctypes.byref(fd), 1, 1)
     rc = lib.mvm_scan_fused_bwd(ctypes.byref(fd), *([fake] * 19), ws, need, null)
     assert rc == _lib.MVM_ERR_INVALID_ARG and "z strides" in _lib.last_error()
+
+
+def test_noalloc_backward_rejects_before_touching_the_gpu():
+    """mvm_scan_bwd_noalloc: a missing checkpoint and a shape whose scratch
+    need exceeds the static array fail on the host, before any device call."""
+    lib = _lib.lib()
+    cap = lib.mvm_scan_noalloc_scratch_bytes()
+    assert cap == 64 * 1024 * 1024
+    fake, null = ctypes.c_void_p(0x1000), ctypes.c_void_p(0)
+    d = _desc(B=2, L=196, D=1536, N=16)
+    args = [fake] * 6 + [null] + [fake] * 8
+    assert lib.mvm_scan_bwd_noalloc(ctypes.byref(d), *args, null) == _lib.MVM_ERR_INVALID_ARG
+    assert "ckpt" in _lib.last_error()
+    big = _desc(B=8, L=16384, D=1536, N=16)
+    assert lib.mvm_scan_workspace_bytes(ctypes.byref(big), 1) > cap
+    rc = lib.mvm_scan_bwd_noalloc(ctypes.byref(big), *([fake] * 15), null)
+    assert rc == _lib.MVM_ERR_WORKSPACE and "static array" in _lib.last_error()
+    # the shapes it is sized for fit
+    step = _desc(B=32, L=196, D=768, N=16, K=4)
+    assert 0 < lib.mvm_scan_workspace_bytes(ctypes.byref(step), 1) <= cap
+    assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), 1) <= cap
