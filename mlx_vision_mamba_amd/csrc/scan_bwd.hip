@@ -50,7 +50,7 @@ namespace mvm {
 
 // Pass 1: adjoint aggregate of chunks 1..nchunk-1: the mu that leaves the
 // chunk's first position when mu = 0 enters its last, and sum(delta).
-template <typename XT, bool FUSE, bool TOK>
+template <typename XT, bool FUSE, bool TOK, typename IdxT>
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   __shared__ float sD[2][kSub][kChPerBlock];
@@ -66,18 +66,21 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int64_t dld = ch0 + lane;
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
+  const int lc = cok ? lane : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
   const int64_t chunk = blockIdx.z + 1;
-  const int64_t t0 = chunk * gm.chunk_len;
-  const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
+  const int32_t L = static_cast<int32_t>(gm.L);
+  const int N = static_cast<int>(gm.N);
+  const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
+  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
   const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
-  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;
-  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;
-  const int64_t bcbase = b * gm.bsb + k * gm.bsk;
-  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
-  const XT* __restrict__ dy = static_cast<const XT*>(bf.dy);
+  const float* __restrict__ delta = bf.delta + (b * gm.dsb + k * gm.dsk + ch0);
+  const XT* __restrict__ dy = static_cast<const XT*>(bf.dy) + (b * gm.ysb + k * gm.ysk + ch0);
+  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm) + (b * gm.bsb + k * gm.bsk);
+  const IdxT sd = static_cast<IdxT>(gm.dst), sy = static_cast<IdxT>(gm.yst);
+  const IdxT sz = static_cast<IdxT>(gm.zst), sbc = static_cast<IdxT>(gm.bst);
   const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   auto stage_delta = [&](float (&v)[4]) {
     if (FUSE) {
@@ -86,8 +89,8 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
     }
   };
   // fused gate: the scan's upstream gradient is dy * silu(z)
-  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;
   const bool gate = FUSE && bf.z != nullptr;
+  const float* __restrict__ zin = gate ? bf.z + (b * gm.zsb + k * gm.zsk + ch0) : nullptr;
   float pz[4] = {0.f, 0.f, 0.f, 0.f};
   auto stage_g = [&](float (&gv)[4]) {
     if (gate) {
@@ -100,24 +103,24 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
+    a2[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
     mu[j] = 0.f;
   }
   float dsum = 0.f;
-  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
+  const int32_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pd[4], pg[4], pc;
-  auto load_tile = [&](int64_t ts) {
-    const TileRows rows = tile_rows<TOK>(tok, ts, gm.L, tid);
-    load_xtile(pd, bf.delta, dbase, rows, gm.dst, lane, cok);
-    load_xtile(pg, dy, ybase, rows, gm.yst, lane, cok);
-    if (gate) load_xtile(pz, bf.z, zbase, rows, gm.zst, lane, cok);
-    pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
+  auto load_tile = [&](int32_t ts) {
+    const TileRows rows = tile_rows<TOK>(tok, ts, L, tid);
+    load_rows(pd, delta, rows, sd, lc);
+    load_rows(pg, dy, rows, sy, lc);
+    if (gate) load_rows(pz, zin, rows, sz, lc);
+    pc = load_state(Cm, rows, sbc, N, tid);
   };
   auto store_tile = [&](int buf) {
     mask_xtile(pd, cok);
     mask_xtile(pg, cok);
     if (gate) mask_xtile(pz, cok);
-    pc = mask_stile(pc, gm.N, tid);
+    pc = mask_stile(pc, N, tid);
     stage_delta(pd);
     stage_g(pg);
     store_xtile(sD[buf], pd, tid);
@@ -126,10 +129,10 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   };
   load_tile(t0 + (ntile - 1) * kSub);
   store_tile(0);
-  for (int64_t j = 0; j < ntile; ++j) {
-    const int buf = static_cast<int>(j & 1);
-    const int64_t ts = t0 + (ntile - 1 - j) * kSub;
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
+  for (int32_t j = 0; j < ntile; ++j) {
+    const int buf = j & 1;
+    const int32_t ts = t0 + (ntile - 1 - j) * kSub;
+    const int nt = min(kSub, t1 - ts);
     __syncthreads();
     const bool more = j + 1 < ntile;
     if (more) load_tile(ts - kSub);
@@ -185,8 +188,9 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
 
 // Pass 2: the reverse sweep.  Each 16-step tile is processed as two 8-step
 // halves (later half first), each restarted from its checkpoint, so the
-// register tile is 9 x 4 states + 8 x 4 decays.
-template <typename XT, typename OT, bool FUSE, bool TOK, bool FOLD>
+// register tile is 9 x 4 states + 8 x 4 decays.  IdxT is the row-offset
+// type (see scan_common.h).
+template <typename XT, typename OT, bool FUSE, bool TOK, bool FOLD, typename IdxT>
 __global__ void __launch_bounds__(kThreads, 2)
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
@@ -211,24 +215,28 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
   const int64_t dc = dvalid ? d : 0;
+  const int lc = cok ? lane : 0;  // channel this thread stages / flushes (0 when out of range)
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
   const int64_t chunk = blockIdx.z;
-  const int64_t t0 = chunk * gm.chunk_len;
-  const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
+  const int32_t L = static_cast<int32_t>(gm.L);
+  const int N = static_cast<int>(gm.N);
+  const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
+  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
   const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
-  // row-independent offsets (including the block's first channel)
-  const int64_t xbase = b * gm.xsb + k * gm.xsk + ch0;
-  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;
-  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;
-  const int64_t bcbase = b * gm.bsb + k * gm.bsk;
-
-  const XT* __restrict__ u = static_cast<const XT*>(bf.u);
-  const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm);
-  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
-  const XT* __restrict__ dy = static_cast<const XT*>(bf.dy);
-  OT* __restrict__ du_out = static_cast<OT*>(bf.du);
+  // the block's first channel of its (b, k) slab in every tensor, and the
+  // row strides in IdxT
+  const XT* __restrict__ u = static_cast<const XT*>(bf.u) + (b * gm.xsb + k * gm.xsk + ch0);
+  const float* __restrict__ delta = bf.delta + (b * gm.dsb + k * gm.dsk + ch0);
+  const XT* __restrict__ dy = static_cast<const XT*>(bf.dy) + (b * gm.ysb + k * gm.ysk + ch0);
+  OT* __restrict__ du_out = static_cast<OT*>(bf.du) + (b * gm.xsb + k * gm.xsk + ch0);
+  float* __restrict__ dd_out = bf.ddelta + (b * gm.dsb + k * gm.dsk + ch0);
+  const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm) + (b * gm.bsb + k * gm.bsk);
+  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm) + (b * gm.bsb + k * gm.bsk);
+  const IdxT sx = static_cast<IdxT>(gm.xst), sd = static_cast<IdxT>(gm.dst);
+  const IdxT sy = static_cast<IdxT>(gm.yst), sz = static_cast<IdxT>(gm.zst);
+  const IdxT sbc = static_cast<IdxT>(gm.bst);
 
   float a2[4], an[4], mu[4];
   double dacc[4];
@@ -236,7 +244,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    an[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) : 0.f;
+    an[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) : 0.f;
     a2[j] = an[j] * kLog2e;
     mu[j] = 0.f;
     dacc[j] = 0.0;
@@ -249,10 +257,10 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       for (int64_t c = gm.nchunk - 1; c > chunk; --c) {
         const int64_t sc = s0 + c * gm.D;
         const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + sc * kStatePad + 4 * grp);
-        const float sd = bf.agg_s[sc];
+        const float sdl = bf.agg_s[sc];
         const float m[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sd), mu[j], m[j]);
+        for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sdl), mu[j], m[j]);
       }
     } else {  // folded by scan_bwd_carry_kernel
       const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + slot * kStatePad + 4 * grp);
@@ -263,13 +271,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   double dDacc = 0.0;
   // state j = (lane >> 4) & 3 of the lane's group holds its channel sum
   const int red_j = (lane >> 4) & 3;
+  // checkpoint slot s of this lane's channel: ckb[s * ck_stride]
   const float* ckb = bf.ckpt + (bk * gm.nck * gm.D + dc) * kStatePad + 4 * grp;
-  const int64_t ck_stride = gm.D * kStatePad;
+  const IdxT ck_stride = static_cast<IdxT>(gm.D * kStatePad);
 
   // state after position p - 1 (checkpoint slot p / 8 - 1), p a multiple of 8
-  auto load_ckpt = [&](int64_t p) {
+  auto load_ckpt = [&](int32_t p) {
     float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p > 0 && dvalid) h4 = *reinterpret_cast<const float4*>(ckb + (p / kCk - 1) * ck_stride);
+    if (p > 0 && dvalid) h4 = *reinterpret_cast<const float4*>(ckb + static_cast<IdxT>(p / kCk - 1) * ck_stride);
     return h4;
   };
   // fused: the dt bias of the channel this thread stages / flushes, and its
@@ -285,8 +294,11 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // fused gate: the upstream dy is the gradient of y_raw * silu(z); the scan
   // consumes g = dy * silu(z) and dz = dy * y_raw * silu'(z) leaves from the
   // staging registers of the tile (rows ts + tt, tt = wave + 4r)
-  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;
   const bool gate = FUSE && bf.z != nullptr;
+  const int64_t zoff = b * gm.zsb + k * gm.zsk + ch0;
+  const float* __restrict__ zin = gate ? bf.z + zoff : nullptr;
+  float* __restrict__ dz_out = gate ? bf.dz + zoff : nullptr;
+  const float* __restrict__ yraw = gate ? bf.y_raw + (b * gm.ysb + k * gm.ysk + ch0) : nullptr;
   float pz[4] = {0.f, 0.f, 0.f, 0.f}, pyr[4] = {0.f, 0.f, 0.f, 0.f};
   auto stage_gate = [&](float (&gv)[4], const TileRows& rows, int nt) {
     if (gate) {
@@ -297,13 +309,15 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float dzv = gv[r] * pyr[r] * (sg * fmaf(pz[r], 1.f - sg, 1.f));
         gv[r] *= pz[r] * sg;
         const int tt = wrow + 4 * r;
-        if (tt < nt && cok) bf.dz[zbase + static_cast<int64_t>(rows.r[r]) * gm.zst + lane] = dzv;
+        if (tt < nt && cok) dz_out[static_cast<IdxT>(rows.r[r]) * sz + lc] = dzv;
       }
     }
   };
+  // this block's dB | dC partial rows: (position, dB|dC, state)
+  float* __restrict__ pbc_blk = bf.part_bc + (bk * gm.ncblk + blockIdx.x) * gm.L * (2 * kStatePad);
   // write back du / ddelta rows (token rows `rows`) and this block's dB | dC
   // partials of a tile
-  auto flush = [&](int buf, const TileRows& rows, int64_t ts, int nt) {
+  auto flush = [&](int buf, const TileRows& rows, int32_t ts, int nt) {
     const int wrow = __builtin_amdgcn_readfirstlane(wave);
     float dbt = 0.f;
 #pragma unroll
@@ -311,7 +325,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       const int tt = wrow + 4 * r;
       if (tt < nt) {
         // values first (no divergent branch); only the stores are masked
-        const int64_t row = rows.r[r];
+        const IdxT row = static_cast<IdxT>(rows.r[r]);
         const float duv = sU[buf][tt][lane];
         float dd = sG[buf][tt][lane];
         if (FUSE) {
@@ -319,13 +333,13 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
           dbt += cok ? dd : 0.f;
         }
         if (cok) {
-          st(du_out + (xbase + row * gm.xst), lane, duv);
-          bf.ddelta[dbase + row * gm.dst + lane] = dd;
+          st(du_out + row * sx, lc, duv);
+          dd_out[row * sd + lc] = dd;
         }
       }
     }
     if (FUSE) dbacc += static_cast<double>(dbt);
-    float* pbc = bf.part_bc + ((bk * gm.ncblk + blockIdx.x) * gm.L + ts) * (2 * kStatePad);
+    float* pbc = pbc_blk + static_cast<IdxT>(ts) * (2 * kStatePad);
     for (int i = tid; i < nt * 2 * kStatePad; i += kThreads) {
       const int tt = i / (2 * kStatePad);
       const int w2 = (i / kStatePad) & 1;
@@ -405,19 +419,19 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     }
   };
 
-  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
+  const int32_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pu[4], pd[4], pg[4], pb, pc;
   float4 pck0, pck1;  // checkpoints entering the two halves of the staged tile
-  auto load_tile = [&](const TileRows& rows, int64_t ts) {
-    load_xtile(pu, u, xbase, rows, gm.xst, lane, cok);
-    load_xtile(pd, bf.delta, dbase, rows, gm.dst, lane, cok);
-    load_xtile(pg, dy, ybase, rows, gm.yst, lane, cok);
+  auto load_tile = [&](const TileRows& rows, int32_t ts) {
+    load_rows(pu, u, rows, sx, lc);
+    load_rows(pd, delta, rows, sd, lc);
+    load_rows(pg, dy, rows, sy, lc);
     if (gate) {
-      load_xtile(pz, bf.z, zbase, rows, gm.zst, lane, cok);
-      load_xtile(pyr, bf.y_raw, ybase, rows, gm.yst, lane, cok);
+      load_rows(pz, zin, rows, sz, lc);
+      load_rows(pyr, yraw, rows, sy, lc);
     }
-    pb = load_stile(Bm, bcbase, rows, gm.bst, gm.N, tid);
-    pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
+    pb = load_state(Bm, rows, sbc, N, tid);
+    pc = load_state(Cm, rows, sbc, N, tid);
     pck0 = load_ckpt(ts);
     pck1 = load_ckpt(ts + kCk);
   };
@@ -430,8 +444,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       mask_xtile(pz, cok);
       mask_xtile(pyr, cok);
     }
-    pb = mask_stile(pb, gm.N, tid);
-    pc = mask_stile(pc, gm.N, tid);
+    pb = mask_stile(pb, N, tid);
+    pc = mask_stile(pc, N, tid);
     stage_delta(pd);
     stage_gate(pg, rows, nt);
     store_xtile(sU[buf], pu, tid);
@@ -442,24 +456,24 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   };
   TileRows rc, rp;  // rows of the tile being computed, of the one before it
   {
-    const int64_t ts = t0 + (ntile - 1) * kSub;
-    rc = tile_rows<TOK>(tok, ts, gm.L, tid);
+    const int32_t ts = t0 + (ntile - 1) * kSub;
+    rc = tile_rows<TOK>(tok, ts, L, tid);
     rp = rc;
     load_tile(rc, ts);
-    store_tile(0, rc, static_cast<int>(t1 - ts));
+    store_tile(0, rc, t1 - ts);
   }
 
-  for (int64_t j = 0; j < ntile; ++j) {
-    const int buf = static_cast<int>(j & 1);
-    const int64_t ts = t0 + (ntile - 1 - j) * kSub;
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
+  for (int32_t j = 0; j < ntile; ++j) {
+    const int buf = j & 1;
+    const int32_t ts = t0 + (ntile - 1 - j) * kSub;
+    const int nt = min(kSub, t1 - ts);
     __syncthreads();  // tile j staged; the previous tile's outputs are complete
-    if (j > 0) flush(buf ^ 1, rp, ts + kSub, static_cast<int>(min<int64_t>(kSub, t1 - ts - kSub)));
+    if (j > 0) flush(buf ^ 1, rp, ts + kSub, min(kSub, t1 - ts - kSub));
     const float4 hin0 = pck0, hin1 = pck1;
     const bool more = j + 1 < ntile;
     TileRows rn = rc;
     if (more) {  // prefetch the previous tile (next in processing order)
-      rn = tile_rows<TOK>(tok, ts - kSub, gm.L, tid);
+      rn = tile_rows<TOK>(tok, ts - kSub, L, tid);
       load_tile(rn, ts - kSub);
     }
     // per-tile partial sums of dA / dD, folded into float64 once per tile
@@ -484,7 +498,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     rc = rn;
   }
   __syncthreads();
-  flush(static_cast<int>((ntile - 1) & 1), rp, t0, static_cast<int>(min<int64_t>(kSub, t1 - t0)));
+  flush((ntile - 1) & 1, rp, t0, min(kSub, t1 - t0));
 
   if (dvalid) {
     double* pa = bf.part_dA + slot * kStatePad + 4 * grp;
@@ -628,13 +642,13 @@ reduce_grads_kernel(Geom gm, BwdBufs bf, int64_t nbc_blocks) {
     reduce_ad_part(gm, bf, blk - nbc_blocks, sq);  // block-uniform branch: its barrier is safe
 }
 
-template <typename XT, typename OT, bool FUSE, bool TOK>
-static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) {
+template <typename XT, typename OT, bool FUSE, bool TOK, typename IdxT>
+static hipError_t launch_bwd_tti(const Geom& g, const BwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE, TOK>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_bwd_agg_kernel<XT, FUSE, TOK, IdxT>), grid_agg, block, 0, s, g, b);
     if (g.nchunk > kFoldMax) {
       const int64_t total = g.B * g.K * g.D * kStatePad;
       hipLaunchKernelGGL(scan_bwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
@@ -646,14 +660,20 @@ static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) 
   // the in-sweep fold is a separate instantiation: the one-chunk and
   // carry-pass kernels carry no code for it
   if (g.nchunk > 1 && g.nchunk <= kFoldMax)
-    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, true>), grid, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, true, IdxT>), grid, block, 0, s, g, b);
   else
-    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, false>), grid, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_bwd_kernel<XT, OT, FUSE, TOK, false, IdxT>), grid, block, 0, s, g, b);
   const int64_t nbc_blocks = g.B * g.K * ((g.L * 2 * kStatePad + kThreads - 1) / kThreads);
   const int64_t nad_blocks = (g.K * g.D * (kStatePad + 2) + 63) / 64;
   hipLaunchKernelGGL((reduce_grads_kernel<OT>), dim3(static_cast<unsigned>(nbc_blocks + nad_blocks)),
                      block, 0, s, g, b, nbc_blocks);
   return hipGetLastError();
+}
+
+template <typename XT, typename OT, bool FUSE, bool TOK>
+static hipError_t launch_bwd_tt(const Geom& g, const BwdBufs& b, hipStream_t s) {
+  return offsets_fit_i32(g) ? launch_bwd_tti<XT, OT, FUSE, TOK, int32_t>(g, b, s)
+                            : launch_bwd_tti<XT, OT, FUSE, TOK, int64_t>(g, b, s);
 }
 
 // remapped (seq_to_tok given) and identity-order instantiations

@@ -204,34 +204,43 @@ struct TileRows {
 };
 
 // Rows of a wave's 4 positions of the tile starting at ts.  Positions past
-// L are clamped to L - 1: their values are staged but never used.
+// L are clamped to L - 1: their values are staged but never used.  All in
+// 32 bits (L < 2^31): wave-uniform values stay in SGPRs, with no 64-bit
+// compares (which the scalar unit lacks) moved onto the VALU.
 template <bool TOK>
-__device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int64_t ts, int64_t L, int tid) {
-  const int wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
+__device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int32_t ts, int32_t L, int tid) {
+  const int32_t wrow = __builtin_amdgcn_readfirstlane(tid >> 6);
   TileRows t;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t p = ts + wrow + 4 * r;
-    t.r[r] = row_of<TOK>(tok, p < L ? p : L - 1, L);
+    const int32_t p = ts + wrow + 4 * r;
+    const int32_t pc = p < L ? p : L - 1;
+    if constexpr (TOK) {
+      const int32_t v = ((const const_i32*)tok)[pc];
+      t.r[r] = v < 0 ? 0 : (v >= L ? L - 1 : v);
+    } else {
+      t.r[r] = pc;
+    }
   }
   return t;
 }
 
-// Channel-indexed tile rows: v[r] = p[base + rows.r[r] * st + lane] (base
-// includes the block's first channel).  Out-of-range channels (cok false)
-// read channel 0 of the row, always in bounds, so no load waits behind a
-// divergent branch; their values are zeroed by mask_xtile when the tile is
-// staged.  Nothing here consumes the loaded values, so a prefetch issued
-// before a tile's math is not waited for until the next tile is staged.
-template <typename T>
-__device__ __forceinline__ void load_xtile(float (&v)[4], const T* __restrict__ p, int64_t base,
-                                           const TileRows& rows, int64_t st, int lch, bool cok) {
-  const int lc = cok ? lch : 0;
+// Row offsets are computed in IdxT: int32_t when every offset of the call
+// within one (batch, direction) slab fits in 31 bits (checked on the host;
+// 32-bit scalar multiplies, no 64-bit pairs held across the loop), else
+// int64_t.  `p` points at the block's first channel of its (b, k) slab.
+
+// Channel-indexed tile rows: v[r] = p[rows.r[r] * st + lc], lc = the
+// lane's channel, or channel 0 for out-of-range channels (always in bounds,
+// so no load waits behind a divergent branch; mask_xtile zeroes them when
+// the tile is staged).  Nothing here consumes the loaded values, so a
+// prefetch issued before a tile's math is not waited for until the next
+// tile is staged.
+template <typename T, typename IdxT>
+__device__ __forceinline__ void load_rows(float (&v)[4], const T* __restrict__ p, const TileRows& rows,
+                                          IdxT st, int lc) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const T* rowp = p + (base + static_cast<int64_t>(rows.r[r]) * st);  // SGPR pointer
-    v[r] = to_f32(rowp[lc]);
-  }
+  for (int r = 0; r < 4; ++r) v[r] = to_f32(p[static_cast<IdxT>(rows.r[r]) * st + lc]);
 }
 __device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
 #pragma unroll
@@ -242,16 +251,14 @@ __device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
 __device__ __forceinline__ int stile_row(int tid) { return (tid >> 6) + 4 * ((tid >> 4) & 3); }
 
 // State-indexed tile value of this thread: state tid & 15 of row
-// stile_row(tid); states >= N read state 0 and are zeroed by mask_stile
-// when the tile is staged.
-template <typename T>
-__device__ __forceinline__ float load_stile(const T* __restrict__ p, int64_t base,
-                                            const TileRows& rows, int64_t st, int64_t N, int tid) {
+// stile_row(tid), from p at the (b, k) slab's start; states >= N read
+// state 0 and are zeroed by mask_stile when the tile is staged.
+template <typename T, typename IdxT>
+__device__ __forceinline__ float load_state(const T* __restrict__ p, const TileRows& rows, IdxT st,
+                                            int N, int tid) {
   const int q = (tid >> 4) & 3, n = tid & 15;
-  const int64_t o0 = static_cast<int64_t>(rows.r[0]) * st, o1 = static_cast<int64_t>(rows.r[1]) * st;
-  const int64_t o2 = static_cast<int64_t>(rows.r[2]) * st, o3 = static_cast<int64_t>(rows.r[3]) * st;
-  const int64_t off = q == 0 ? o0 : (q == 1 ? o1 : (q == 2 ? o2 : o3));
-  return ld(p, base + off + (n < N ? n : 0));
+  const int32_t row = q == 0 ? rows.r[0] : (q == 1 ? rows.r[1] : (q == 2 ? rows.r[2] : rows.r[3]));
+  return to_f32(p[static_cast<IdxT>(row) * st + (n < N ? n : 0)]);
 }
 __device__ __forceinline__ float mask_stile(float x, int64_t N, int tid) {
   return (tid & 15) < N ? x : 0.f;

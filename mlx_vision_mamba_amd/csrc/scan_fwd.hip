@@ -41,7 +41,7 @@ namespace mvm {
 
 enum FwdMode { kAgg = 0, kMain = 1 };
 
-template <typename XT, typename OT, int MODE, bool FUSE, bool TOK>
+template <typename XT, typename OT, int MODE, bool FUSE, bool TOK, typename IdxT>
 __global__ void __launch_bounds__(kThreads, 6)
 scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // double-buffered tile staging: u, delta (64 channels), B, C (16 states);
@@ -63,36 +63,37 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
   const int64_t dc = dvalid ? d : 0;
+  const int lc = cok ? lane : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
   const int64_t chunk = blockIdx.z;
-  const int64_t t0 = chunk * gm.chunk_len;
-  const int64_t t1 = min(gm.L, t0 + gm.chunk_len);
+  const int32_t L = static_cast<int32_t>(gm.L);
+  const int N = static_cast<int>(gm.N);
+  const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
+  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
   const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
-  // row-independent offsets (including the block's first channel)
-  const int64_t xbase = b * gm.xsb + k * gm.xsk + ch0;     // u
-  const int64_t dbase = b * gm.dsb + k * gm.dsk + ch0;     // delta
-  const int64_t ybase = b * gm.ysb + k * gm.ysk + ch0;     // y, y_raw
-  const int64_t zbase = b * gm.zsb + k * gm.zsk + ch0;     // gate
-  const int64_t bcbase = b * gm.bsb + k * gm.bsk;
-
-  const XT* __restrict__ u = static_cast<const XT*>(bf.u);
-  const float* __restrict__ delta = bf.delta;
-  const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm);
-  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm);
-  OT* __restrict__ y = static_cast<OT*>(bf.y);
-  float* __restrict__ ckpt = bf.ckpt;
+  // the block's first channel of its (b, k) slab in every tensor
+  const XT* __restrict__ u = static_cast<const XT*>(bf.u) + (b * gm.xsb + k * gm.xsk + ch0);
+  const float* __restrict__ delta = bf.delta + (b * gm.dsb + k * gm.dsk + ch0);
+  const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm) + (b * gm.bsb + k * gm.bsk);
+  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm) + (b * gm.bsb + k * gm.bsk);
+  const int64_t yoff = b * gm.ysb + k * gm.ysk + ch0;
+  OT* __restrict__ y = bf.y != nullptr ? static_cast<OT*>(bf.y) + yoff : nullptr;
+  const IdxT sx = static_cast<IdxT>(gm.xst), sd = static_cast<IdxT>(gm.dst);
+  const IdxT sy = static_cast<IdxT>(gm.yst), sz = static_cast<IdxT>(gm.zst);
+  const IdxT sbc = static_cast<IdxT>(gm.bst);
   // fused prologue: the dt bias of the channel this thread stages
   const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   const bool gate = FUSE && MODE == kMain && bf.z != nullptr;
-  float* __restrict__ y_raw = FUSE ? bf.y_raw : nullptr;
+  const float* __restrict__ zin = gate ? bf.z + (b * gm.zsb + k * gm.zsk + ch0) : nullptr;
+  float* __restrict__ y_raw = (FUSE && bf.y_raw != nullptr) ? bf.y_raw + yoff : nullptr;
 
   float a2[4], h[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < gm.N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
+    a2[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
     h[j] = 0.f;
   }
   const float dskip = (MODE == kMain && dvalid) ? bf.Dv[k * gm.D + d] : 0.f;
@@ -105,10 +106,10 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       for (int64_t c = 0; c < chunk; ++c) {
         const int64_t sc = s0 + c * gm.D;
         const float4 e4 = *reinterpret_cast<const float4*>(bf.agg_h + sc * kStatePad + 4 * grp);
-        const float sd = bf.agg_s[sc];
+        const float sdl = bf.agg_s[sc];
         const float e[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) h[j] = fmaf(fast_exp2(a2[j] * sd), h[j], e[j]);
+        for (int j = 0; j < 4; ++j) h[j] = fmaf(fast_exp2(a2[j] * sdl), h[j], e[j]);
       }
     } else {  // folded by scan_fwd_carry_kernel
       const float4 c4 = *reinterpret_cast<const float4*>(bf.agg_h + slot * kStatePad + 4 * grp);
@@ -117,10 +118,10 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   }
   float dsum = 0.f;
   const bool write_y = MODE == kMain && y != nullptr;
-  const bool write_ck = MODE == kMain && ckpt != nullptr && dvalid;
+  const bool write_ck = MODE == kMain && bf.ckpt != nullptr && dvalid;
   // checkpoint slot s holds the state after position 8s + 7
-  float* ckp = write_ck ? ckpt + (bk * gm.nck * gm.D + d) * kStatePad + 4 * grp : nullptr;
-  const int64_t ck_stride = gm.D * kStatePad;
+  float* ckp = write_ck ? bf.ckpt + (bk * gm.nck * gm.D + d) * kStatePad + 4 * grp : nullptr;
+  const IdxT ck_stride = static_cast<IdxT>(gm.D * kStatePad);
   // y of a staged tile (held in sU, token rows `rows`) back to HBM; zv = the
   // gate values of the same rows and channel when fused
   auto flush_y = [&](int buf, const TileRows& rows, int nt, const float (&zv)[4]) {
@@ -129,11 +130,11 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     for (int r = 0; r < 4; ++r) {
       const int tt = wrow + 4 * r;
       if (tt < nt && cok) {
-        const int64_t roff = static_cast<int64_t>(rows.r[r]) * gm.yst;
+        const IdxT roff = static_cast<IdxT>(rows.r[r]) * sy;
         float v = sU[buf][tt][lane];
-        if (FUSE && y_raw != nullptr) y_raw[ybase + roff + lane] = v;
+        if (FUSE && y_raw != nullptr) y_raw[roff + lc] = v;
         if (gate) v *= zv[r] * sigmoid_f(zv[r]);
-        st(y + (ybase + roff), lane, v);
+        st(y + roff, lc, v);
       }
     }
   };
@@ -169,22 +170,23 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       sU[buf][tt][cl] = fmaf(dskip, uu, yp);  // in place: u_t is consumed
     }
   };
-  auto store_ck = [&](int64_t pos_end) {  // state after position pos_end (== 8s + 7)
-    *reinterpret_cast<float4*>(ckp + (pos_end / kCk) * ck_stride) = make_float4(h[0], h[1], h[2], h[3]);
+  auto store_ck = [&](int32_t pos_end) {  // state after position pos_end (== 8s + 7)
+    *reinterpret_cast<float4*>(ckp + static_cast<IdxT>(pos_end / kCk) * ck_stride) =
+        make_float4(h[0], h[1], h[2], h[3]);
   };
   auto load_tile = [&](const TileRows& rows, float (&pu)[4], float (&pd)[4], float& pb, float& pc) {
-    load_xtile(pu, u, xbase, rows, gm.xst, lane, cok);
-    load_xtile(pd, delta, dbase, rows, gm.dst, lane, cok);
-    pb = load_stile(Bm, bcbase, rows, gm.bst, gm.N, tid);
-    if (MODE == kMain) pc = load_stile(Cm, bcbase, rows, gm.bst, gm.N, tid);
+    load_rows(pu, u, rows, sx, lc);
+    load_rows(pd, delta, rows, sd, lc);
+    pb = load_state(Bm, rows, sbc, N, tid);
+    if (MODE == kMain) pc = load_state(Cm, rows, sbc, N, tid);
   };
   // zero the out-of-range channels / states of a prefetched tile: the first
   // use of its values, after the current tile's math
   auto mask_tile = [&](float (&pu)[4], float (&pd)[4], float& pb, float& pc) {
     mask_xtile(pu, cok);
     mask_xtile(pd, cok);
-    pb = mask_stile(pb, gm.N, tid);
-    pc = mask_stile(pc, gm.N, tid);
+    pb = mask_stile(pb, N, tid);
+    pc = mask_stile(pc, N, tid);
   };
   auto store_tile = [&](int buf, const float (&pu)[4], const float (&pd)[4], float pb, float pc) {
     store_xtile(sU[buf], pu, tid);
@@ -193,27 +195,27 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
     sC[buf][stile_row(tid)][tid & 15] = pc;
   };
 
-  const int64_t ntile = (t1 - t0 + kSub - 1) / kSub;
+  const int32_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pu[4], pd[4], pz[4] = {0.f, 0.f, 0.f, 0.f}, pb = 0.f, pc = 0.f;
-  TileRows rc = tile_rows<TOK>(tok, t0, gm.L, tid);  // rows of the tile being computed
-  TileRows rp = rc;                                   // rows of the previous tile
+  TileRows rc = tile_rows<TOK>(tok, t0, L, tid);  // rows of the tile being computed
+  TileRows rp = rc;                                // rows of the previous tile
   load_tile(rc, pu, pd, pb, pc);
   mask_tile(pu, pd, pb, pc);
   stage_delta(pd);
   store_tile(0, pu, pd, pb, pc);
 
-  for (int64_t it = 0; it < ntile; ++it) {
-    const int buf = static_cast<int>(it & 1);
-    const int64_t ts = t0 + it * kSub;
-    const int nt = static_cast<int>(min<int64_t>(kSub, t1 - ts));
+  for (int32_t it = 0; it < ntile; ++it) {
+    const int buf = it & 1;
+    const int32_t ts = t0 + it * kSub;
+    const int nt = min(kSub, t1 - ts);
     __syncthreads();  // tile `it` staged; readers of the other buffer are done
     if (write_y && it > 0) flush_y(buf ^ 1, rp, kSub, pz);
     // gate values of this tile, used when it is flushed one tile later
-    if (gate) load_xtile(pz, bf.z, zbase, rc, gm.zst, lane, cok);
+    if (gate) load_rows(pz, zin, rc, sz, lc);
     const bool more = it + 1 < ntile;
     TileRows rn = rc;
     if (more) {  // prefetch the next tile; its latency overlaps this tile's math
-      rn = tile_rows<TOK>(tok, ts + kSub, gm.L, tid);
+      rn = tile_rows<TOK>(tok, ts + kSub, L, tid);
       load_tile(rn, pu, pd, pb, pc);
     }
     if (nt == kSub) {  // full tile: no per-step bounds checks
@@ -238,8 +240,8 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   }
   if (write_y) {
     __syncthreads();
-    const int64_t ts = t0 + (ntile - 1) * kSub;
-    flush_y(static_cast<int>((ntile - 1) & 1), rp, static_cast<int>(t1 - ts), pz);
+    const int32_t ts = t0 + (ntile - 1) * kSub;
+    flush_y((ntile - 1) & 1, rp, t1 - ts, pz);
   }
 
   if (MODE == kAgg && dvalid) {
@@ -274,13 +276,13 @@ scan_fwd_carry_kernel(Geom gm, FwdBufs bf) {
   }
 }
 
-template <typename XT, typename OT, bool FUSE, bool TOK>
-static hipError_t launch_fwd_tt(const Geom& g, const FwdBufs& b, hipStream_t s) {
+template <typename XT, typename OT, bool FUSE, bool TOK, typename IdxT>
+static hipError_t launch_fwd_tti(const Geom& g, const FwdBufs& b, hipStream_t s) {
   const dim3 block(kThreads);
   if (g.nchunk > 1) {
     const dim3 grid_agg(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                         static_cast<unsigned>(g.nchunk - 1));
-    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE, TOK>), grid_agg, block, 0, s, g, b);
+    hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kAgg, FUSE, TOK, IdxT>), grid_agg, block, 0, s, g, b);
     if (g.nchunk > kFoldMax) {
       const int64_t total = g.B * g.K * g.D * kStatePad;
       hipLaunchKernelGGL(scan_fwd_carry_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
@@ -289,8 +291,14 @@ static hipError_t launch_fwd_tt(const Geom& g, const FwdBufs& b, hipStream_t s) 
   }
   const dim3 grid(static_cast<unsigned>(g.ncblk), static_cast<unsigned>(g.B * g.K),
                   static_cast<unsigned>(g.nchunk));
-  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain, FUSE, TOK>), grid, block, 0, s, g, b);
+  hipLaunchKernelGGL((scan_fwd_kernel<XT, OT, kMain, FUSE, TOK, IdxT>), grid, block, 0, s, g, b);
   return hipGetLastError();
+}
+
+template <typename XT, typename OT, bool FUSE, bool TOK>
+static hipError_t launch_fwd_tt(const Geom& g, const FwdBufs& b, hipStream_t s) {
+  return offsets_fit_i32(g) ? launch_fwd_tti<XT, OT, FUSE, TOK, int32_t>(g, b, s)
+                            : launch_fwd_tti<XT, OT, FUSE, TOK, int64_t>(g, b, s);
 }
 
 // remapped (seq_to_tok given) and identity-order instantiations

@@ -23,6 +23,18 @@ struct Geom {
   int32_t a_log;           // 1: the A array holds A_log, A = -exp(A_log)
 };
 
+// True when every row offset the kernels form within one (batch,
+// direction) slab fits in int32 (row strides, the checkpoint and partial
+// rows included), so that they use the 32-bit row arithmetic; else the
+// int64 instantiations run.
+inline bool offsets_fit_i32(const Geom& g) {
+  constexpr int64_t lim = INT32_MAX - 64;  // head-room for the lane's channel
+  const int64_t lm = g.L > 0 ? g.L - 1 : 0;
+  auto ok = [&](int64_t st) { return st >= 0 && st <= lim && lm * st <= lim; };
+  return ok(g.xst) && ok(g.dst) && ok(g.yst) && ok(g.zst) && ok(g.bst) &&
+         g.nck * g.D * 16 <= lim && g.L * 2 * 16 <= lim;  // 16 states per channel
+}
+
 struct FwdBufs {
   const void* u;
   const float* delta;
