@@ -240,7 +240,7 @@ template <typename T, typename IdxT>
 __device__ __forceinline__ void load_rows(float (&v)[4], const T* __restrict__ p, const TileRows& rows,
                                           IdxT st, int lc) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = to_f32(p[static_cast<IdxT>(rows.r[r]) * st + lc]);
+  for (int r = 0; r < 4; ++r) v[r] = to_f32((p + static_cast<IdxT>(rows.r[r]) * st)[lc]);
 }
 __device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
 #pragma unroll
@@ -258,7 +258,7 @@ __device__ __forceinline__ float load_state(const T* __restrict__ p, const TileR
                                             int N, int tid) {
   const int q = (tid >> 4) & 3, n = tid & 15;
   const int32_t row = q == 0 ? rows.r[0] : (q == 1 ? rows.r[1] : (q == 2 ? rows.r[2] : rows.r[3]));
-  return to_f32(p[static_cast<IdxT>(row) * st + (n < N ? n : 0)]);
+  return to_f32((p + static_cast<IdxT>(row) * st)[n < N ? n : 0]);
 }
 __device__ __forceinline__ float mask_stile(float x, int64_t N, int tid) {
   return (tid & 15) < N ? x : 0.f;

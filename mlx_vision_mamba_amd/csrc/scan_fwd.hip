@@ -132,7 +132,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
       if (tt < nt && cok) {
         const IdxT roff = static_cast<IdxT>(rows.r[r]) * sy;
         float v = sU[buf][tt][lane];
-        if (FUSE && y_raw != nullptr) y_raw[roff + lc] = v;
+        if (FUSE && y_raw != nullptr) (y_raw + roff)[lc] = v;
         if (gate) v *= zv[r] * sigmoid_f(zv[r]);
         st(y + roff, lc, v);
       }

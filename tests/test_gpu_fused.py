@@ -167,3 +167,35 @@ def test_fused_equals_unfused_composition(cuda):
                               bc[..., 22:].to(cuda), c["Dv"].to(cuda),
                               torch.tensor(c["tok"], device=cuda))
     torch.testing.assert_close(y, y2, rtol=1e-5, atol=1e-5)
+
+
+def test_fused_64bit_row_offsets(cuda):
+    """Row offsets beyond int32 inside one (batch, direction) slab (z and dz
+    rows 2^25 floats apart, an 8.6 GB span) run the int64 instantiations of
+    the kernels; they equal the int32 kernels on the same values bitwise."""
+    from mlx_vision_mamba_amd import scan
+    print("case: fused scan with z rows 2^25 floats apart (int64 offsets)", flush=True)
+    bsz, L, K, D, N = 1, 65, 1, 64, 16
+    gen = torch.Generator().manual_seed(77)
+    u = torch.randn(bsz, L, K, D, generator=gen).to(cuda)
+    draw = (torch.randn(bsz, L, K, D, generator=gen) - 3.0).to(cuda)
+    bias = torch.randn(K, D, generator=gen).to(cuda) * 0.3
+    A = -torch.exp(torch.randn(K, D, N, generator=gen) * 0.5).to(cuda)
+    Bm = torch.randn(bsz, L, K, N, generator=gen).to(cuda)
+    Cm = torch.randn(bsz, L, K, N, generator=gen).to(cuda)
+    Dv = torch.randn(K, D, generator=gen).to(cuda)
+    z = torch.randn(bsz, L, K, D, generator=gen).to(cuda)
+    g = torch.randn(bsz, L, K, D, generator=gen).to(cuda)
+    big = torch.empty(L, 1 << 25, device=cuda)
+    zs = big[:, :D].view(bsz, L, K, D)        # row stride 2^25
+    zs.copy_(z)
+    assert zs.stride(1) == 1 << 25
+    outs = []
+    for zz in (z, zs):
+        y, y_raw, ck = scan.scan_fused_forward(u, draw, bias, A, Bm, Cm, Dv, zz, save=True)
+        grads = scan.scan_fused_backward(u, draw, bias, A, Bm, Cm, Dv, zz, y_raw, ck, g)
+        outs.append([y] + [t for t in grads if t is not None])
+        torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert torch.equal(a, b.contiguous()), f"output {i}"
+    del big
