@@ -186,6 +186,89 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     return value_region, region, per, mode
 
 
+ENCODERS = {
+    # name: (input shape, model kwargs); seeds 2 / 1002 and 3 / 1003 (inputs / weights)
+    "3d_K6_B4_128cube": ((4, 128, 128, 128, 1),
+                         dict(img_size=128, patch_size=8, input_dim=3), 2),
+    "4d_K8_B2_T8_64cube": ((2, 8, 64, 64, 64, 1),
+                           dict(img_size=64, patch_size=16, input_dim=4, num_temporal_frames=8,
+                                temporal_patch_size=1), 3),
+}
+
+
+def bench_encoder(torch, mvm, scan, name, steps, warmup, device):
+    """Train step of the 3D (K=6) or 4D (K=8) VisionMamba encoder
+    (vision_mamba.py:156-171): E=384, d_state 16, depth 6, float32,
+    synthetic N(0,1) volumes, loss = mean of the output features, AdamW.
+    Timed as `steps` replays of the captured step (ms/step, volumes/s), and
+    the scan's share from HIP events around every fused scan call of
+    `steps` eager steps."""
+    shape, kw, seed = ENCODERS[name]
+    torch.manual_seed(1000 + seed)
+    model = mvm.VisionMamba(in_channels=1, embed_dim=384, depth=6, d_state=16, scan_mode="hip",
+                            **kw).to(device)
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(device)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=True)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 3)):
+            opt.zero_grad(set_to_none=True)
+            model(x).mean().backward()
+            opt.step()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    opt.zero_grad(set_to_none=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        model(x).mean().backward()
+        opt.step()
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    del g
+    # eager steps with every scan launch timed on its stream
+    opt_e = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    for _ in range(2):
+        opt_e.zero_grad(set_to_none=True)
+        model(x).mean().backward()
+        opt_e.step()
+    torch.cuda.synchronize()
+    records = []
+    scan.set_scan_timing(records)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        opt_e.zero_grad(set_to_none=True)
+        loss = model(x).mean()
+        loss.backward()
+        opt_e.step()
+    torch.cuda.synchronize()
+    eager = time.perf_counter() - t1
+    scan.set_scan_timing(None)
+    if not math.isfinite(float(loss.detach())):
+        raise RuntimeError(f"{name}: non-finite loss")
+    t_f = sum(e0.elapsed_time(e1) for k, e0, e1, _ in records if k == "fwd") * 1e-3 / steps
+    t_b = sum(e0.elapsed_time(e1) for k, e0, e1, _ in records if k == "bwd") * 1e-3 / steps
+    b_f = sum(nb for k, _, _, nb in records if k == "fwd") / steps
+    b_b = sum(nb for k, _, _, nb in records if k == "bwd") / steps
+    ms = elapsed / steps * 1e3
+    L = model.num_patches
+    return {"workload": f"VisionMamba {kw['input_dim']}D K={model.num_directions} train step "
+                        f"(fwd + mean loss + bwd + AdamW)",
+            "input": "x".join(str(v) for v in shape), "seq_len": L, "directions": model.num_directions,
+            "embed_dim": 384, "depth": 6, "steps": steps, "ms_per_step": round(ms, 3),
+            "samples_per_s": round(shape[0] / (ms * 1e-3), 2),
+            "eager_ms_per_step": round(eager / steps * 1e3, 3),
+            "scan_fwd_ms_per_step": round(t_f * 1e3, 3), "scan_bwd_ms_per_step": round(t_b * 1e3, 3),
+            "scan_share_of_eager_step": round((t_f + t_b) / (eager / steps), 3),
+            "scan_GBps": round((b_f + b_b) / (t_f + t_b) / 1e9, 1),
+            "scan_chunk_len": int(scan.chunk_len_for(shape[0] * model.num_directions, L, 768))}
+
+
 def copy_bandwidth(torch, device, iters=20):
     """Measured HBM bandwidth of a plain 512 MiB device-to-device copy
     (torch's copy kernel: 512 MiB read + 512 MiB written per copy), timed
@@ -277,6 +360,8 @@ def bench_scan(torch, scan, bsz, L, D, N, dtype, iters, device):
         tg = (time.perf_counter() - t0) / iters
         out["graph_fwd_vjp_us"] = round(tg * 1e6, 2)
         out["graph_GBps"] = round((bf + bb) / tg / 1e9, 1)
+        out["graph_pct_hbm_peak"] = round((bf + bb) / tg / 1e9 / HBM_PEAK_GBS * 100, 2)
+        out["graph_tokens_per_s"] = round(bsz * L / tg, 1)
     except RuntimeError as err:
         print(f"bench.py: scan graph capture failed ({err})", file=sys.stderr, flush=True)
     return out
@@ -354,6 +439,34 @@ def scan_driver_long(torch, scan, device):
     print(json.dumps({"scan_driver": "done", "shape": "B=8 L=16384 D=1536 N=16 bf16"}), flush=True)
 
 
+def scan_driver_small(torch, scan, device):
+    """Profiling driver (--scan-driver-small): the single-block scan at B=2,
+    L=196, D=1536, N=16 fp32, forward + VJP captured in one HIP graph and
+    replayed 20 times (the launch sequence of the graph figure of the bench
+    line's single-block entry)."""
+    from mlx_vision_mamba_amd import synthetic as scan_inputs
+    u, dl, A, Bm, Cm, Dv, g = [t.to(device) for t in scan_inputs.make(2, 196, 1536, 16, seed=0)]
+    args = (u.unsqueeze(2), dl.unsqueeze(2), A.unsqueeze(0), Bm.unsqueeze(2), Cm.unsqueeze(2),
+            Dv.unsqueeze(0))
+    g4 = g.unsqueeze(2)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        y, ck = scan.scan_forward(*args, save_ckpt=True)
+        scan.scan_backward(*args, g4, ckpt=ck)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y, ck = scan.scan_forward(*args, save_ckpt=True)
+        scan.scan_backward(*args, g4, ckpt=ck)
+    for _ in range(20):
+        graph.replay()
+    torch.cuda.synchronize()
+    print(json.dumps({"scan_driver": "done", "shape": "B=2 L=196 D=1536 N=16 fp32, 20 graph replays"}),
+          flush=True)
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")
 
 
@@ -392,15 +505,33 @@ def cpu_baseline(torch):
         out.mean().backward()
 
     step()  # warm-up
-    t0 = time.perf_counter()
-    step()
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
     scan_cpu = cpu_scan_baseline(torch)
     return {"value": round(2 / dt, 3), "unit": "imgs/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": "VisionMamba-2D K=4 step (fwd + mean loss + bwd), batch 2 of the same "
                       "224x224x1 / patch 16 / E=384 / depth 6 model, float32, reference's "
-                      "sequential scan restated in torch; 1 warm-up + 1 timed step",
-            "seconds_per_step": round(dt, 2), "scan": scan_cpu}
+                      "sequential scan restated in torch; 1 warm-up, median of 3 timed steps",
+            "seconds_per_step": round(dt, 2), "step_seconds": [round(t, 2) for t in times],
+            "scan": scan_cpu}
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
 
 
 def cpu_scan_baseline(torch):
@@ -473,6 +604,11 @@ def main():
     ap.add_argument("--scan-driver-long", action="store_true",
                     help="profiling driver only: a 512 MiB copy + 2 plain scan fwd/VJP calls at "
                          "B=8 L=16384 D=1536 N=16 bf16")
+    ap.add_argument("--scan-driver-small", action="store_true",
+                    help="profiling driver only: 20 graph replays of the scan fwd/VJP pair at "
+                         "B=2 L=196 D=1536 N=16 fp32")
+    ap.add_argument("--no-encoders", action="store_true",
+                    help="skip the 3D (K=6) and 4D (K=8) encoder steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the selective-scan path is benchmarked on a "
@@ -492,6 +628,9 @@ def main():
         return
     if args.scan_driver_long:
         scan_driver_long(torch, scan, device)
+        return
+    if args.scan_driver_small:
+        scan_driver_small(torch, scan, device)
         return
     if args.tune_gemms:
         gemm_tuning.start_tuning(args.tune_gemms)
@@ -554,6 +693,9 @@ def main():
         "roofline": roofline,
         "scan": scans,
     }
+    if not args.no_encoders:
+        out["encoders"] = {name: bench_encoder(torch, mvm, scan, name, 5, 2, device)
+                           for name in ENCODERS}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(out), flush=True)

@@ -538,6 +538,18 @@ def get_scan_fn(scan_mode: str):
         raise ValueError(f"unknown scan_mode {scan_mode!r}; expected one of {SCAN_MODES}") from None
 
 
+def chunk_len_for(rows, L, D, N=16):
+    """Time-chunk length the library picks for `rows` = batch x directions
+    scans of length L over D channels (the whole sequence when it is one
+    chunk)."""
+    d = _lib.ScanDesc()
+    d.batch, d.seqlen, d.dim, d.dstate, d.ndir = rows, L, D, N, 1
+    d.x_stride_b, d.x_stride_k, d.x_stride_t = L * D, 0, D
+    d.bc_stride_b, d.bc_stride_k, d.bc_stride_t = L * N, 0, N
+    d.in_dtype = d.out_dtype = _lib.MVM_F32
+    return _lib.check(_lib.lib().mvm_scan_chunk_len(ctypes.byref(d)))
+
+
 def mode_chunk_len(scan_mode: str):
     get_scan_fn(scan_mode)
     return _MODE_CHUNK[scan_mode]
