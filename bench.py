@@ -4,6 +4,7 @@ scan's fwd+VJP bandwidth, printed as one JSON line.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--eager]
     python bench.py --scan-driver     (profiling driver, see scan_driver)
     python bench.py --scan-driver-long  (profiling driver, see scan_driver_long)
+    python bench.py --scan-driver-small  (profiling driver, see scan_driver_small)
 
 Workload (the step timed): VisionMamba encoder, 2D, K=4 scan directions,
 batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
@@ -49,6 +50,9 @@ D=1536, N=16 fp32 and at B=8, L=16384, D=1536, N=16 with bf16 u/B/C/y/grads,
 timed over back-to-back calls with inputs resident in HBM (events split
 the stream time between forward and VJP), and as replays of the pair
 captured in a HIP graph (graph_fwd_vjp_us: no host time between launches).
+The long entry carries each pass's VALUBusy from the committed counter
+summary (valu_busy_per_pass): every pass is bound by VALU issue, so the
+distance to that bound, not to the HBM peak, is what remains.
 
 cpu_baseline: the oracle's CPU restatement of the reference's sequential
 VisionMamba step (materialised discretisation, Python time loop, autograd)
@@ -468,15 +472,17 @@ def scan_driver_small(torch, scan, device):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "scan_visionmamba_shape_traffic_pmc.md")
+LONG_PROFILE = os.path.join(ROOT, "profiles", "scan_long_bf16_pmc.md")
+LONG_PASSES = ("fwd_aggregate", "fwd_main", "bwd_aggregate", "bwd_main")
 
 
-def measured_traffic(key, kind=int):
-    """A figure measured with rocprofv3 counters on the scan at the
-    VisionMamba step shape (a line `key: <value>` of the committed profile
-    summary: HBM bytes per call from FETCH_SIZE / WRITE_SIZE, or the
-    backward's VALU busy fraction from the VALUBusy counter), or None."""
+def measured_traffic(key, kind=int, path=TRAFFIC_PROFILE):
+    """A figure measured with rocprofv3 counters (a line `key: <value>` of a
+    committed profile summary: HBM bytes per call from FETCH_SIZE /
+    WRITE_SIZE, or a kernel's VALU busy fraction from the VALUBusy counter;
+    by default the scan at the VisionMamba step shape), or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith(key + ":"):
                     return kind(line.split(":", 1)[1].split()[0])
@@ -672,6 +678,10 @@ def main():
         "single_block_B2_L196": bench_scan(torch, scan, 2, 196, 1536, 16, torch.float32, 200, device),
         "long_B8_L16384_bf16": bench_scan(torch, scan, 8, 16384, 1536, 16, torch.bfloat16, 5, device),
     }
+    # each pass of the long scan is VALU-issue bound: the share of its cycles
+    # the SIMDs' VALU is issuing (VALUBusy counter, committed profile)
+    scans["long_B8_L16384_bf16"]["valu_busy_per_pass"] = {
+        p: measured_traffic("long_valu_busy_" + p, float, LONG_PROFILE) for p in LONG_PASSES}
     out = {
         "metric": METRIC, "value": round(imgs, 2), "unit": "imgs/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
