@@ -190,18 +190,35 @@ scan_bwd_carry_kernel(Geom gm, BwdBufs bf) {
 // halves (later half first), each restarted from its checkpoint, so the
 // register tile is 9 x 4 states + 8 x 4 decays.  IdxT is the row-offset
 // type (see scan_common.h).
+//
+// Two resident-wave budgets.  The plain 32-bit-offset sweep (the long
+// sequences) is built lean for 3 waves per SIMD (<= 168 VGPRs): its float64
+// dA / dD sums live in LDS, its per-wave dB | dC channel sums are single-
+// buffered (summed right after the tile's second barrier), delta * u and A
+// are re-formed where they are used, and the next tile's two checkpoints are
+// loaded one half-sweep apart.  The fused sweep (the block's scan, with the
+// softplus / gate gradients) and the 64-bit-offset sweep hold more state and
+// run at 2 waves per SIMD, where those trades cost more than they return.
+template <bool FUSE, typename IdxT>
+constexpr bool bwd_lean() {
+  return !FUSE && std::is_same<IdxT, int32_t>::value;
+}
 template <typename XT, typename OT, bool FUSE, bool TOK, bool FOLD, typename IdxT>
-__global__ void __launch_bounds__(kThreads, 2)
+__global__ void __launch_bounds__(kThreads, (bwd_lean<FUSE, IdxT>() ? 3 : 2))
 scan_bwd_kernel(Geom gm, BwdBufs bf) {
+  constexpr bool kLean = bwd_lean<FUSE, IdxT>();
   // double-buffered tile staging (u, delta, dy, B, C); du / ddelta are
   // written in place over u / dy of the same step once it is consumed (delta
   // stays for the fused softplus gradient); per-wave channel sums of dB | dC
+  // (one buffer when lean); lean: each thread's float64 dA (4 states) and dD
+  // running sums
   __shared__ float sU[2][kSub][kChPerBlock];
   __shared__ float sD[2][kSub][kChPerBlock];
   __shared__ float sG[2][kSub][kChPerBlock];
   __shared__ float sB[2][kSub][kStatePad];
   __shared__ float sC[2][kSub][kStatePad];
-  __shared__ float sRed[2][4][kSub][2][kStatePad];
+  __shared__ float sRed[kLean ? 1 : 2][4][kSub][2][kStatePad];
+  __shared__ double sAcc[5][kLean ? kThreads : 1];
   __shared__ double sDb[4][kChPerBlock];  // fused: per-wave dt_bias gradient sums
 
   const int tid = threadIdx.x;
@@ -238,8 +255,10 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const IdxT sy = static_cast<IdxT>(gm.yst), sz = static_cast<IdxT>(gm.zst);
   const IdxT sbc = static_cast<IdxT>(gm.bst);
 
+  // an = A (unused when lean: the sweep sums w * A * log2(e) and scales the
+  // sum by ln 2 instead), a2 = A * log2(e)
   float a2[4], an[4], mu[4];
-  double dacc[4];
+  double dacc[4], dDacc = 0.0;  // not lean: float64 dA / dD running sums
   const int64_t slot = (bk * gm.nchunk + chunk) * gm.D + dc;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -248,6 +267,10 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     a2[j] = an[j] * kLog2e;
     mu[j] = 0.f;
     dacc[j] = 0.0;
+  }
+  if constexpr (kLean) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) sAcc[j][tid] = 0.0;
   }
   if (chunk + 1 < gm.nchunk && dvalid) {
     if constexpr (FOLD) {
@@ -268,17 +291,19 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     }
   }
   const float dskip = dvalid ? bf.Dv[k * gm.D + d] : 0.f;
-  double dDacc = 0.0;
   // state j = (lane >> 4) & 3 of the lane's group holds its channel sum
   const int red_j = (lane >> 4) & 3;
-  // checkpoint slot s of this lane's channel: ckb[s * ck_stride]
-  const float* ckb = bf.ckpt + (bk * gm.nck * gm.D + dc) * kStatePad + 4 * grp;
-  const IdxT ck_stride = static_cast<IdxT>(gm.D * kStatePad);
+  // checkpoint slot s of this lane's channel: float4 (cl * 4 + grp) of row s
+  // (stride D * 16 floats) from the block's first channel
+  const float4* ckb = reinterpret_cast<const float4*>(bf.ckpt + (bk * gm.nck * gm.D + ch0) * kStatePad);
+  const IdxT ck_stride = static_cast<IdxT>(gm.D * (kStatePad / 4));
+  const int ck_lane = cl * 4 + grp;
+  const uint32_t ck_lane_b = static_cast<uint32_t>(ck_lane) * 16u;
 
   // state after position p - 1 (checkpoint slot p / 8 - 1), p a multiple of 8
   auto load_ckpt = [&](int32_t p) {
     float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p > 0 && dvalid) h4 = *reinterpret_cast<const float4*>(ckb + static_cast<IdxT>(p / kCk - 1) * ck_stride);
+    if (p > 0 && dvalid) h4 = row_elem(ckb, p / kCk - 1, ck_stride, ck_lane, ck_lane_b);
     return h4;
   };
   // fused: the dt bias of the channel this thread stages / flushes, and its
@@ -295,6 +320,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // consumes g = dy * silu(z) and dz = dy * y_raw * silu'(z) leaves from the
   // staging registers of the tile (rows ts + tt, tt = wave + 4r)
   const bool gate = FUSE && bf.z != nullptr;
+  const uint32_t lb4 = static_cast<uint32_t>(lc) * 4u;  // byte offset of the lane's channel (fp32)
   const int64_t zoff = b * gm.zsb + k * gm.zsk + ch0;
   const float* __restrict__ zin = gate ? bf.z + zoff : nullptr;
   float* __restrict__ dz_out = gate ? bf.dz + zoff : nullptr;
@@ -309,15 +335,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float dzv = gv[r] * pyr[r] * (sg * fmaf(pz[r], 1.f - sg, 1.f));
         gv[r] *= pz[r] * sg;
         const int tt = wrow + 4 * r;
-        if (tt < nt && cok) (dz_out + static_cast<IdxT>(rows.r[r]) * sz)[lc] = dzv;
+        if (tt < nt && cok) row_elem(dz_out, rows.r[r], sz, lc, lb4) = dzv;
       }
     }
   };
   // this block's dB | dC partial rows: (position, dB|dC, state)
   float* __restrict__ pbc_blk = bf.part_bc + (bk * gm.ncblk + blockIdx.x) * gm.L * (2 * kStatePad);
-  // write back du / ddelta rows (token rows `rows`) and this block's dB | dC
-  // partials of a tile
-  auto flush = [&](int buf, const TileRows& rows, int32_t ts, int nt) {
+  // write back the du / ddelta rows of a tile (token rows `rows`)
+  auto flush = [&](int buf, const TileRows& rows, int nt) {
     const int wrow = __builtin_amdgcn_readfirstlane(wave);
     float dbt = 0.f;
 #pragma unroll
@@ -325,7 +350,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       const int tt = wrow + 4 * r;
       if (tt < nt) {
         // values first (no divergent branch); only the stores are masked
-        const IdxT row = static_cast<IdxT>(rows.r[r]);
+        const int32_t row = rows.r[r];
         const float duv = sU[buf][tt][lane];
         float dd = sG[buf][tt][lane];
         if (FUSE) {
@@ -333,19 +358,23 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
           dbt += cok ? dd : 0.f;
         }
         if (cok) {
-          st(du_out + row * sx, lc, duv);
-          (dd_out + row * sd)[lc] = dd;
+          row_elem(du_out, row, sx, lc, static_cast<uint32_t>(lc * sizeof(OT))) = from_f32<OT>(duv);
+          row_elem(dd_out, row, sd, lc, lb4) = dd;
         }
       }
     }
     if (FUSE) dbacc += static_cast<double>(dbt);
+  };
+  // this block's dB | dC partials of a tile: the 4 waves' channel sums in
+  // sRed[rb], added in a fixed order
+  auto flush_red = [&](int rb, int32_t ts, int nt) {
     float* pbc = pbc_blk + static_cast<IdxT>(ts) * (2 * kStatePad);
     for (int i = tid; i < nt * 2 * kStatePad; i += kThreads) {
       const int tt = i / (2 * kStatePad);
       const int w2 = (i / kStatePad) & 1;
       const int n = i % kStatePad;
-      pbc[i] = (sRed[buf][0][tt][w2][n] + sRed[buf][1][tt][w2][n]) +
-               (sRed[buf][2][tt][w2][n] + sRed[buf][3][tt][w2][n]);
+      pbc[i] = (sRed[rb][0][tt][w2][n] + sRed[rb][1][tt][w2][n]) +
+               (sRed[rb][2][tt][w2][n] + sRed[rb][3][tt][w2][n]);
     }
   };
 
@@ -357,14 +386,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     constexpr bool kFull = decltype(full)::value;
     float hs[kCk + 1][4];
     float ea[kCk][4];
-    float dxs[kCk];  // delta * u of each step, reused by the reverse loop
+    float dxs[kCk];  // delta * u of each step, reused by the reverse loop (not lean)
     hs[0][0] = hin.x; hs[0][1] = hin.y; hs[0][2] = hin.z; hs[0][3] = hin.w;
 #pragma unroll
     for (int i = 0; i < kCk; ++i) {
       const int tt = h0 + i;
       const float dl = sD[buf][tt][cl];
       const float dxu = dl * sU[buf][tt][cl];
-      dxs[i] = dxu;
+      if constexpr (!kLean) dxs[i] = dxu;
       const float4 b4 = *reinterpret_cast<const float4*>(&sB[buf][tt][4 * grp]);
       const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
@@ -388,7 +417,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float4 c4 = *reinterpret_cast<const float4*>(&sC[buf][tt][4 * grp]);
         const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
         const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
-        const float dxu = dxs[i];
+        const float dxu = kLean ? dl * uu : dxs[i];
         float sa = 0.f, sb = 0.f;
         float xb[4], xc[4];
 #pragma unroll
@@ -396,14 +425,14 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
           const float lam = fmaf(cv[jj], gy, mu[jj]);
           const float q = lam * ea[i][jj];
           const float w = q * hs[i][jj];
-          sa = fmaf(w, an[jj], sa);
+          sa = fmaf(w, kLean ? a2[jj] : an[jj], sa);
           tacc[jj] = fmaf(w, dl, tacc[jj]);
           sb = fmaf(lam, bv[jj], sb);
           xb[jj] = lam * dxu;
           xc[jj] = gy * hs[i + 1][jj];
           mu[jj] = q;
         }
-        sa = sum_groups(sa);
+        sa = kLean ? sum_groups(sa) * kLn2 : sum_groups(sa);
         sb = sum_groups(sb);
         tD = fmaf(gy, uu, tD);
         // in place: this step's u / dy are consumed (the 4 lanes of the
@@ -413,15 +442,17 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float rb = channel_reduce4(xb[0], xb[1], xb[2], xb[3]);
         const float rc = channel_reduce4(xc[0], xc[1], xc[2], xc[3]);
         // lanes with equal (g, j) hold equal sums and store them together
-        sRed[buf][wave][tt][0][4 * grp + red_j] = rb;
-        sRed[buf][wave][tt][1][4 * grp + red_j] = rc;
+        sRed[kLean ? 0 : buf][wave][tt][0][4 * grp + red_j] = rb;
+        sRed[kLean ? 0 : buf][wave][tt][1][4 * grp + red_j] = rc;
       }
     }
   };
 
   const int32_t ntile = (t1 - t0 + kSub - 1) / kSub;
   float pu[4], pd[4], pg[4], pb, pc;
-  float4 pck0, pck1;  // checkpoints entering the two halves of the staged tile
+  // checkpoints entering the two halves of the staged tile (lean: the next
+  // tile's pck0 is loaded after the first half-sweep, not with the prefetch)
+  float4 pck0, pck1;
   auto load_tile = [&](const TileRows& rows, int32_t ts) {
     load_rows(pu, u, rows, sx, lc);
     load_rows(pd, delta, rows, sd, lc);
@@ -432,7 +463,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     }
     pb = load_state(Bm, rows, sbc, N, tid);
     pc = load_state(Cm, rows, sbc, N, tid);
-    pck0 = load_ckpt(ts);
+    if constexpr (!kLean) pck0 = load_ckpt(ts);
     pck1 = load_ckpt(ts + kCk);
   };
   auto store_tile = [&](int buf, const TileRows& rows, int nt) {
@@ -460,6 +491,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     rc = tile_rows<TOK>(tok, ts, L, tid);
     rp = rc;
     load_tile(rc, ts);
+    if constexpr (kLean) pck0 = load_ckpt(ts);
     store_tile(0, rc, t1 - ts);
   }
 
@@ -468,7 +500,10 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     const int32_t ts = t0 + (ntile - 1 - j) * kSub;
     const int nt = min(kSub, t1 - ts);
     __syncthreads();  // tile j staged; the previous tile's outputs are complete
-    if (j > 0) flush(buf ^ 1, rp, ts + kSub, min(kSub, t1 - ts - kSub));
+    if (j > 0) {
+      flush(buf ^ 1, rp, min(kSub, t1 - ts - kSub));
+      if constexpr (!kLean) flush_red(buf ^ 1, ts + kSub, min(kSub, t1 - ts - kSub));
+    }
     const float4 hin0 = pck0, hin1 = pck1;
     const bool more = j + 1 < ntile;
     TileRows rn = rc;
@@ -487,30 +522,46 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
       // VisionMamba step shape)
       __builtin_amdgcn_s_setprio(1);
       half(std::true_type{}, buf, kCk, kCk, hin1);
+      if (kLean && more) pck0 = load_ckpt(ts - kSub);
       half(std::true_type{}, buf, 0, kCk, hin0);
       __builtin_amdgcn_s_setprio(0);
     } else {
       if (nt > kCk) half(std::false_type{}, buf, kCk, nt - kCk, hin1);
+      if (kLean && more) pck0 = load_ckpt(ts - kSub);
       half(std::false_type{}, buf, 0, nt < kCk ? nt : kCk, hin0);
     }
+    if constexpr (kLean) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dacc[jj] += static_cast<double>(tacc[jj]);
-    dDacc += static_cast<double>(tD);
-    if (more) {
-      __syncthreads();  // all flushes of the other buffer are done before it is refilled
-      store_tile(buf ^ 1, rn, kSub);
+      for (int jj = 0; jj < 4; ++jj) sAcc[jj][tid] += static_cast<double>(tacc[jj]);
+      sAcc[4][tid] += static_cast<double>(tD);
+      // the tile's dB | dC channel sums are complete and every flush of the
+      // other buffer is done before it is refilled; the staging goes first
+      // (its wait for the prefetched loads would otherwise also wait for
+      // the partials' stores: one in-order counter covers both)
+      __syncthreads();
+      if (more) store_tile(buf ^ 1, rn, kSub);
+      flush_red(0, ts, nt);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dacc[jj] += static_cast<double>(tacc[jj]);
+      dDacc += static_cast<double>(tD);
+      if (more) {
+        __syncthreads();  // all flushes of the other buffer are done before it is refilled
+        store_tile(buf ^ 1, rn, kSub);
+      }
     }
     rp = rc;
     rc = rn;
   }
-  __syncthreads();
-  flush((ntile - 1) & 1, rp, t0, min(kSub, t1 - t0));
+  if constexpr (!kLean) __syncthreads();  // lean: the last tile's second barrier
+  flush((ntile - 1) & 1, rp, min(kSub, t1 - t0));
+  if constexpr (!kLean) flush_red((ntile - 1) & 1, t0, min(kSub, t1 - t0));
 
   if (dvalid) {
     double* pa = bf.part_dA + slot * kStatePad + 4 * grp;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) pa[jj] = dacc[jj];
-    if (grp == 0) bf.part_dD[slot] = dDacc;
+    for (int jj = 0; jj < 4; ++jj) pa[jj] = kLean ? sAcc[jj][tid] : dacc[jj];
+    if (grp == 0) bf.part_dD[slot] = kLean ? sAcc[4][tid] : dDacc;
   }
   if (FUSE && bf.ddbias != nullptr) {  // dt_bias gradient: the 4 waves' rows, fixed order
     sDb[wave][lane] = dbacc;

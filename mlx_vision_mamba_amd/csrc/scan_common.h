@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mvm {
 
 constexpr int kSub = 16;          // scan positions per staged tile
@@ -21,6 +23,7 @@ constexpr int kChPerWave = 16;
 constexpr int kChPerBlock = 64;
 constexpr int kStatePad = 16;     // states per channel in every internal buffer
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 // Up to this many time chunks, each chunk of the main scan folds the chunk
 // aggregates it needs itself (one launch fewer); beyond it a separate carry
 // pass folds them once, so no block waits on a long chain of loads.
@@ -80,7 +83,6 @@ __device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int6
 // < 2^-24 absolute, < 2e-6 relative there).
 // Both branches are evaluated and selected (no divergent control flow).
 __device__ __forceinline__ float log1p_unit(float y) {
-  constexpr float kLn2 = 0.6931471805599453f;
   const float series = y * fmaf(y, fmaf(y, fmaf(y, fmaf(y, 0.2f, -0.25f), 1.f / 3.f), -0.5f), 1.f);
   const float direct = kLn2 * __builtin_amdgcn_logf(1.f + y);
   return y < 0.015625f ? series : direct;
@@ -225,10 +227,31 @@ __device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int32_t ts, in
   return t;
 }
 
-// Row offsets are computed in IdxT: int32_t when every offset of the call
-// within one (batch, direction) slab fits in 31 bits (checked on the host;
-// 32-bit scalar multiplies, no 64-bit pairs held across the loop), else
-// int64_t.  `p` points at the block's first channel of its (b, k) slab.
+// Row offsets are computed in IdxT: int32_t when every element offset of
+// the call within one (batch, direction) slab is below 2^30 (checked on the
+// host), so that its byte offset fits in 32 bits; else int64_t.  `p` points
+// at the block's first channel of its (b, k) slab.
+//
+// In the int32_t instantiations an access is that block-uniform base plus a
+// 32-bit byte offset: the row's part is wave-uniform (a scalar multiply),
+// the lane's part a VGPR, so it compiles to one global access with the base
+// in SGPRs and the offset in a VGPR (saddr form), with no 64-bit per-lane
+// pointer held in VGPRs and no 64-bit address arithmetic on the VALU.
+template <typename T>
+__device__ __forceinline__ T* at_bytes(T* base, uint32_t off) {
+  using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+  return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + off);
+}
+// Element (row, lane) of a slab: p[row * st + lc], with lane_off = lc *
+// sizeof(T) precomputed by the caller for the 32-bit form.
+template <typename T, typename IdxT>
+__device__ __forceinline__ T& row_elem(T* p, int32_t row, IdxT st, int lc, uint32_t lane_off) {
+  if constexpr (std::is_same<IdxT, int32_t>::value) {
+    return *at_bytes(p, static_cast<uint32_t>(row * st) * static_cast<uint32_t>(sizeof(T)) + lane_off);
+  } else {
+    return (p + static_cast<IdxT>(row) * st)[lc];
+  }
+}
 
 // Channel-indexed tile rows: v[r] = p[rows.r[r] * st + lc], lc = the
 // lane's channel, or channel 0 for out-of-range channels (always in bounds,
@@ -239,8 +262,9 @@ __device__ __forceinline__ TileRows tile_rows(const int32_t* tok, int32_t ts, in
 template <typename T, typename IdxT>
 __device__ __forceinline__ void load_rows(float (&v)[4], const T* __restrict__ p, const TileRows& rows,
                                           IdxT st, int lc) {
+  const uint32_t lb = static_cast<uint32_t>(lc) * static_cast<uint32_t>(sizeof(T));
 #pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = to_f32((p + static_cast<IdxT>(rows.r[r]) * st)[lc]);
+  for (int r = 0; r < 4; ++r) v[r] = to_f32(row_elem(p, rows.r[r], st, lc, lb));
 }
 __device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
 #pragma unroll

@@ -28,7 +28,10 @@ struct Geom {
 // rows included), so that they use the 32-bit row arithmetic; else the
 // int64 instantiations run.
 inline bool offsets_fit_i32(const Geom& g) {
-  constexpr int64_t lim = INT32_MAX - 64;  // head-room for the lane's channel
+  // element offsets below 2^30, so that byte offsets (elements of <= 4 bytes,
+  // 16-byte checkpoint groups addressed as floats) fit in 32 bits; head-room
+  // for the lane's channel
+  constexpr int64_t lim = (int64_t{1} << 30) - 64;
   const int64_t lm = g.L > 0 ? g.L - 1 : 0;
   auto ok = [&](int64_t st) { return st >= 0 && st <= lim && lm * st <= lim; };
   return ok(g.xst) && ok(g.dst) && ok(g.yst) && ok(g.zst) && ok(g.bst) &&
