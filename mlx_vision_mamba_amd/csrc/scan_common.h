@@ -277,12 +277,25 @@ __device__ __forceinline__ int stile_row(int tid) { return (tid >> 6) + 4 * ((ti
 // State-indexed tile value of this thread: state tid & 15 of row
 // stile_row(tid), from p at the (b, k) slab's start; states >= N read
 // state 0 and are zeroed by mask_stile when the tile is staged.
+// In the 32-bit form the lane's row is chosen among the wave's four
+// (scalar) rows with two bit-selects and its byte offset formed in a VGPR,
+// so the address is the SGPR base plus one VGPR offset, with no per-lane
+// pointer or branch.
 template <typename T, typename IdxT>
 __device__ __forceinline__ float load_state(const T* __restrict__ p, const TileRows& rows, IdxT st,
                                             int N, int tid) {
   const int q = (tid >> 4) & 3, n = tid & 15;
-  const int32_t row = q == 0 ? rows.r[0] : (q == 1 ? rows.r[1] : (q == 2 ? rows.r[2] : rows.r[3]));
-  return to_f32((p + static_cast<IdxT>(row) * st)[n < N ? n : 0]);
+  const int nc = n < N ? n : 0;
+  if constexpr (std::is_same<IdxT, int32_t>::value) {
+    constexpr uint32_t kSz = static_cast<uint32_t>(sizeof(T));
+    const int32_t lo = (q & 1) ? rows.r[1] : rows.r[0];
+    const int32_t hi = (q & 1) ? rows.r[3] : rows.r[2];
+    const int32_t row = (q & 2) ? hi : lo;
+    return to_f32(*at_bytes(p, static_cast<uint32_t>(row * st + nc) * kSz));
+  } else {
+    const int32_t row = q == 0 ? rows.r[0] : (q == 1 ? rows.r[1] : (q == 2 ? rows.r[2] : rows.r[3]));
+    return to_f32((p + static_cast<IdxT>(row) * st)[nc]);
+  }
 }
 __device__ __forceinline__ float mask_stile(float x, int64_t N, int tid) {
   return (tid & 15) < N ? x : 0.f;
