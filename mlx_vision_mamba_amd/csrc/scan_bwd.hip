@@ -572,8 +572,6 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   }
 }
 
-// dB / dC: sum the channel-block partials in a fixed order and store at the
-// token row each scan position read (mamba_metal_fused.py:221,224).
 // The two fixed-order reductions after the sweep, in one launch: blocks
 // [0, nbc_blocks) reduce dB / dC, the rest dA, dD and the dt bias.
 //

@@ -23,10 +23,10 @@ struct Geom {
   int32_t a_log;           // 1: the A array holds A_log, A = -exp(A_log)
 };
 
-// True when every row offset the kernels form within one (batch,
-// direction) slab fits in int32 (row strides, the checkpoint and partial
-// rows included), so that they use the 32-bit row arithmetic; else the
-// int64 instantiations run.
+// True when every element offset the kernels form within one (batch,
+// direction) slab is below 2^30 (row strides, the checkpoint and partial
+// rows included), so that they use the 32-bit row and byte-offset
+// arithmetic; else the int64 instantiations run.
 inline bool offsets_fit_i32(const Geom& g) {
   // element offsets below 2^30, so that byte offsets (elements of <= 4 bytes,
   // 16-byte checkpoint groups addressed as floats) fit in 32 bits; head-room
