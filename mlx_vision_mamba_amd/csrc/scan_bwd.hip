@@ -545,10 +545,12 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dacc[jj] += static_cast<double>(tacc[jj]);
       dDacc += static_cast<double>(tD);
-      if (more) {
-        __syncthreads();  // all flushes of the other buffer are done before it is refilled
-        store_tile(buf ^ 1, rn, kSub);
-      }
+      // no barrier: each thread refills exactly the LDS slots of the other
+      // buffer that it flushed at this tile's start (its dB | dC sums, read
+      // by every thread, are not refilled), and this tile's math reads only
+      // this buffer; the next tile's first barrier orders the refill before
+      // that buffer's math
+      if (more) store_tile(buf ^ 1, rn, kSub);
     }
     rp = rc;
     rc = rn;
