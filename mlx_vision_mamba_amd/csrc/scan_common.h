@@ -44,15 +44,9 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
-  // round to nearest even; NaN stays NaN (quiet bit forced)
-  uint32_t u = __float_as_uint(v);
+  // round to nearest even, NaN stays NaN: one v_cvt_pk_bf16_f32 on gfx950
   bf16_t r;
-  if ((u & 0x7f800000u) == 0x7f800000u) {
-    r.bits = static_cast<uint16_t>((u >> 16) | ((u & 0x007fffffu) ? 0x0040u : 0u));
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
   return r;
 }
 
