@@ -237,23 +237,23 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t b = bk / gm.K;
   const int64_t k = bk - b * gm.K;
   const int64_t chunk = blockIdx.z;
-  const int32_t L = static_cast<int32_t>(gm.L);
-  const int N = static_cast<int>(gm.N);
-  const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
-  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
-  const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
+  const int32_t L = own_sc(static_cast<int32_t>(gm.L));
+  const int N = own_sc(static_cast<int>(gm.N));
+  const int32_t t0 = own_sc(static_cast<int32_t>(chunk * gm.chunk_len));
+  const int32_t t1 = own_sc(min(L, static_cast<int32_t>(t0 + gm.chunk_len)));
+  const int32_t* tok = TOK ? own_ptr(gm.tok + k * gm.L) : nullptr;
   // the block's first channel of its (b, k) slab in every tensor, and the
   // row strides in IdxT
-  const XT* __restrict__ u = static_cast<const XT*>(bf.u) + (b * gm.xsb + k * gm.xsk + ch0);
-  const float* __restrict__ delta = bf.delta + (b * gm.dsb + k * gm.dsk + ch0);
-  const XT* __restrict__ dy = static_cast<const XT*>(bf.dy) + (b * gm.ysb + k * gm.ysk + ch0);
-  OT* __restrict__ du_out = static_cast<OT*>(bf.du) + (b * gm.xsb + k * gm.xsk + ch0);
-  float* __restrict__ dd_out = bf.ddelta + (b * gm.dsb + k * gm.dsk + ch0);
-  const XT* __restrict__ Bm = static_cast<const XT*>(bf.Bm) + (b * gm.bsb + k * gm.bsk);
-  const XT* __restrict__ Cm = static_cast<const XT*>(bf.Cm) + (b * gm.bsb + k * gm.bsk);
-  const IdxT sx = static_cast<IdxT>(gm.xst), sd = static_cast<IdxT>(gm.dst);
-  const IdxT sy = static_cast<IdxT>(gm.yst), sz = static_cast<IdxT>(gm.zst);
-  const IdxT sbc = static_cast<IdxT>(gm.bst);
+  const XT* __restrict__ u = own_ptr(static_cast<const XT*>(bf.u) + (b * gm.xsb + k * gm.xsk + ch0));
+  const float* __restrict__ delta = own_ptr(bf.delta + (b * gm.dsb + k * gm.dsk + ch0));
+  const XT* __restrict__ dy = own_ptr(static_cast<const XT*>(bf.dy) + (b * gm.ysb + k * gm.ysk + ch0));
+  OT* __restrict__ du_out = own_ptr(static_cast<OT*>(bf.du) + (b * gm.xsb + k * gm.xsk + ch0));
+  float* __restrict__ dd_out = own_ptr(bf.ddelta + (b * gm.dsb + k * gm.dsk + ch0));
+  const XT* __restrict__ Bm = own_ptr(static_cast<const XT*>(bf.Bm) + (b * gm.bsb + k * gm.bsk));
+  const XT* __restrict__ Cm = own_ptr(static_cast<const XT*>(bf.Cm) + (b * gm.bsb + k * gm.bsk));
+  const IdxT sx = own_sc(static_cast<IdxT>(gm.xst)), sd = own_sc(static_cast<IdxT>(gm.dst));
+  const IdxT sy = own_sc(static_cast<IdxT>(gm.yst)), sz = own_sc(static_cast<IdxT>(gm.zst));
+  const IdxT sbc = own_sc(static_cast<IdxT>(gm.bst));
 
   // an = A (unused when lean: the sweep sums w * A * log2(e) and scales the
   // sum by ln 2 instead), a2 = A * log2(e)
@@ -295,8 +295,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int red_j = (lane >> 4) & 3;
   // checkpoint slot s of this lane's channel: float4 (cl * 4 + grp) of row s
   // (stride D * 16 floats) from the block's first channel
-  const float4* ckb = reinterpret_cast<const float4*>(bf.ckpt + (bk * gm.nck * gm.D + ch0) * kStatePad);
-  const IdxT ck_stride = static_cast<IdxT>(gm.D * (kStatePad / 4));
+  const float4* ckb = own_ptr(reinterpret_cast<const float4*>(bf.ckpt + (bk * gm.nck * gm.D + ch0) * kStatePad));
+  const IdxT ck_stride = own_sc(static_cast<IdxT>(gm.D * (kStatePad / 4)));
   const int ck_lane = cl * 4 + grp;
   const uint32_t ck_lane_b = static_cast<uint32_t>(ck_lane) * 16u;
 
@@ -322,9 +322,9 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const bool gate = FUSE && bf.z != nullptr;
   const uint32_t lb4 = static_cast<uint32_t>(lc) * 4u;  // byte offset of the lane's channel (fp32)
   const int64_t zoff = b * gm.zsb + k * gm.zsk + ch0;
-  const float* __restrict__ zin = gate ? bf.z + zoff : nullptr;
-  float* __restrict__ dz_out = gate ? bf.dz + zoff : nullptr;
-  const float* __restrict__ yraw = gate ? bf.y_raw + (b * gm.ysb + k * gm.ysk + ch0) : nullptr;
+  const float* __restrict__ zin = gate ? own_ptr(bf.z + zoff) : nullptr;
+  float* __restrict__ dz_out = gate ? own_ptr(bf.dz + zoff) : nullptr;
+  const float* __restrict__ yraw = gate ? own_ptr(bf.y_raw + (b * gm.ysb + k * gm.ysk + ch0)) : nullptr;
   float pz[4] = {0.f, 0.f, 0.f, 0.f}, pyr[4] = {0.f, 0.f, 0.f, 0.f};
   auto stage_gate = [&](float (&gv)[4], const TileRows& rows, int nt) {
     if (gate) {
@@ -340,7 +340,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     }
   };
   // this block's dB | dC partial rows: (position, dB|dC, state)
-  float* __restrict__ pbc_blk = bf.part_bc + (bk * gm.ncblk + blockIdx.x) * gm.L * (2 * kStatePad);
+  float* __restrict__ pbc_blk = own_ptr(bf.part_bc + (bk * gm.ncblk + blockIdx.x) * gm.L * (2 * kStatePad));
   // write back the du / ddelta rows of a tile (token rows `rows`)
   auto flush = [&](int buf, const TileRows& rows, int nt) {
     const int wrow = __builtin_amdgcn_readfirstlane(wave);

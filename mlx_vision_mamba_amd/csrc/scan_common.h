@@ -300,4 +300,20 @@ __device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float
   for (int r = 0; r < 4; ++r) s[(tid >> 6) + 4 * r][tid & 63] = v[r];
 }
 
+// Block-uniform kernel-argument values copied into SGPRs of their own, so
+// that the registers of the 64-byte argument loads they came from do not
+// stay live (and are not spilled whole) across the sweep.  A pointer keeps
+// the global address space.
+template <typename T>
+__device__ __forceinline__ T own_sc(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T* own_ptr(T* p) {
+  uint64_t v = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+s"(v));
+  return (T*)(__attribute__((address_space(1))) T*)v;
+}
+
 }  // namespace mvm
