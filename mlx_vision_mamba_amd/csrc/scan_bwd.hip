@@ -100,10 +100,10 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   };
 
   float a2[4], mu[4];
+  load_ax4(a2, bf.A, (k * gm.D + (dvalid ? d : 0)) * gm.N, grp, N, dvalid, gm.a_log);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
+    a2[j] *= kLog2e;
     mu[j] = 0.f;
   }
   float dsum = 0.f;
@@ -260,10 +260,19 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   float a2[4], an[4], mu[4];
   double dacc[4], dDacc = 0.0;  // not lean: float64 dA / dD running sums
   const int64_t slot = (bk * gm.nchunk + chunk) * gm.D + dc;
+  // the lean sweep issues the 4 A loads together; the 2-wave forms keep the
+  // per-state loads, with which their scalar registers fit without spills
+  if constexpr (kLean) {
+    load_ax4(an, bf.A, (k * gm.D + dc) * gm.N, grp, N, dvalid, gm.a_log);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = 4 * grp + j;
+      an[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) : 0.f;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int n = 4 * grp + j;
-    an[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) : 0.f;
     a2[j] = an[j] * kLog2e;
     mu[j] = 0.f;
     dacc[j] = 0.0;
@@ -275,15 +284,38 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   if (chunk + 1 < gm.nchunk && dvalid) {
     if constexpr (FOLD) {
       // adjoint carry-in: fold the aggregates of chunks nchunk-1 .. chunk+1
-      // right to left, mu = exp(A * S_c) * mu + M_c
+      // right to left, mu = exp(A * S_c) * mu + M_c.  In the 32-bit form
+      // all of them (at most kFoldMax) are loaded first, from in-bounds
+      // chunk indices, so that their latencies overlap; the 64-bit form,
+      // short of scalar registers, loads them one at a time.
       const int64_t s0 = bk * gm.nchunk * gm.D + dc;
-      for (int64_t c = gm.nchunk - 1; c > chunk; --c) {
-        const int64_t sc = s0 + c * gm.D;
-        const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + sc * kStatePad + 4 * grp);
-        const float sdl = bf.agg_s[sc];
-        const float m[4] = {m4.x, m4.y, m4.z, m4.w};
+      if constexpr (std::is_same<IdxT, int32_t>::value) {
+        float4 m4[kFoldMax];
+        float sdl[kFoldMax];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sdl), mu[j], m[j]);
+        for (int i = 0; i < kFoldMax; ++i) {
+          const int64_t c = gm.nchunk - 1 - i;
+          const int64_t sc = s0 + (c >= 0 ? c : 0) * gm.D;
+          m4[i] = *reinterpret_cast<const float4*>(bf.agg_mu + sc * kStatePad + 4 * grp);
+          sdl[i] = bf.agg_s[sc];
+        }
+#pragma unroll
+        for (int i = 0; i < kFoldMax; ++i) {
+          if (gm.nchunk - 1 - i > chunk) {
+            const float m[4] = {m4[i].x, m4[i].y, m4[i].z, m4[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sdl[i]), mu[j], m[j]);
+          }
+        }
+      } else {
+        for (int64_t c = gm.nchunk - 1; c > chunk; --c) {
+          const int64_t sc = s0 + c * gm.D;
+          const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + sc * kStatePad + 4 * grp);
+          const float sdl = bf.agg_s[sc];
+          const float m[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mu[j] = fmaf(fast_exp2(a2[j] * sdl), mu[j], m[j]);
+        }
       }
     } else {  // folded by scan_bwd_carry_kernel
       const float4 m4 = *reinterpret_cast<const float4*>(bf.agg_mu + slot * kStatePad + 4 * grp);

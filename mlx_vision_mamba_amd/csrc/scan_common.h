@@ -108,6 +108,23 @@ __device__ __forceinline__ float load_A(const float* A, int64_t i, int a_log) {
   return a_log ? -expf(v) : v;
 }
 
+// a[j] = A[d, 4g + j] for the 4 states of a lane's group, 0 for states
+// >= N or an invalid channel (A = -exp(A_log) when a_log is set).  The 4
+// loads go to clamped, in-bounds indices and are issued together before
+// any is used (a load under the validity branch would be waited for one at
+// a time: 4 memory latencies in every block's prologue).
+__device__ __forceinline__ void load_ax4(float (&a)[4], const float* A, int64_t row, int grp, int N,
+                                         bool valid, int a_log) {
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = 4 * grp + j;
+    v[j] = A[row + (n < N ? n : 0)];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = (valid && 4 * grp + j < N) ? (a_log ? -expf(v[j]) : v[j]) : 0.f;
+}
+
 // 2^x on the transcendental unit (v_exp_f32); callers pre-scale by log2(e).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

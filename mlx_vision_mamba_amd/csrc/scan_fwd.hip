@@ -90,26 +90,37 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   float* __restrict__ y_raw = (FUSE && bf.y_raw != nullptr) ? bf.y_raw + yoff : nullptr;
 
   float a2[4], h[4];
+  load_ax4(a2, bf.A, (k * gm.D + dc) * gm.N, grp, N, dvalid, gm.a_log);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int n = 4 * grp + j;
-    a2[j] = (dvalid && n < N) ? load_A(bf.A, (k * gm.D + d) * gm.N + n, gm.a_log) * kLog2e : 0.f;
+    a2[j] *= kLog2e;
     h[j] = 0.f;
   }
-  const float dskip = (MODE == kMain && dvalid) ? bf.Dv[k * gm.D + d] : 0.f;
+  const float dskip_v = bf.Dv[k * gm.D + dc];
+  const float dskip = (MODE == kMain && dvalid) ? dskip_v : 0.f;
   const int64_t slot = (bk * gm.nchunk + chunk) * gm.D + dc;  // (bk, chunk, d)
   if (MODE == kMain && chunk > 0 && dvalid) {
     if (gm.nchunk <= kFoldMax) {
       // carry-in: fold the aggregates of chunks 0..chunk-1 left to right,
-      // H = exp(A * S_c) * H + E_c (mamba_fast.py:85-86)
+      // H = exp(A * S_c) * H + E_c (mamba_fast.py:85-86).  All (at most
+      // kFoldMax) aggregates are loaded first, from in-bounds chunk indices,
+      // so their latencies overlap; the fold then runs on registers.
       const int64_t s0 = bk * gm.nchunk * gm.D + dc;
-      for (int64_t c = 0; c < chunk; ++c) {
-        const int64_t sc = s0 + c * gm.D;
-        const float4 e4 = *reinterpret_cast<const float4*>(bf.agg_h + sc * kStatePad + 4 * grp);
-        const float sdl = bf.agg_s[sc];
-        const float e[4] = {e4.x, e4.y, e4.z, e4.w};
+      float4 e4[kFoldMax];
+      float sdl[kFoldMax];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) h[j] = fmaf(fast_exp2(a2[j] * sdl), h[j], e[j]);
+      for (int c = 0; c < kFoldMax; ++c) {
+        const int64_t sc = s0 + (c < gm.nchunk ? c : 0) * gm.D;
+        e4[c] = *reinterpret_cast<const float4*>(bf.agg_h + sc * kStatePad + 4 * grp);
+        sdl[c] = bf.agg_s[sc];
+      }
+#pragma unroll
+      for (int c = 0; c < kFoldMax; ++c) {
+        if (c < chunk) {
+          const float e[4] = {e4[c].x, e4[c].y, e4[c].z, e4[c].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) h[j] = fmaf(fast_exp2(a2[j] * sdl[c]), h[j], e[j]);
+        }
       }
     } else {  // folded by scan_fwd_carry_kernel
       const float4 c4 = *reinterpret_cast<const float4*>(bf.agg_h + slot * kStatePad + 4 * grp);
