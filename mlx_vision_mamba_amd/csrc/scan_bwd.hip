@@ -66,6 +66,7 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int64_t dld = ch0 + lane;
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
+  const bool all_in = ch0 + kChPerBlock <= gm.D;  // block-uniform: no channel masked
   const int lc = cok ? lane : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / gm.K;
@@ -117,9 +118,9 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
     pc = load_state(Cm, rows, sbc, N, tid);
   };
   auto store_tile = [&](int buf) {
-    mask_xtile(pd, cok);
-    mask_xtile(pg, cok);
-    if (gate) mask_xtile(pz, cok);
+    mask_xtile(pd, cok, all_in);
+    mask_xtile(pg, cok, all_in);
+    if (gate) mask_xtile(pz, cok, all_in);
     pc = mask_stile(pc, N, tid);
     stage_delta(pd);
     stage_g(pg);
@@ -231,6 +232,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t dld = ch0 + lane;
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
+  const bool all_in = ch0 + kChPerBlock <= gm.D;  // block-uniform: no channel masked
   const int64_t dc = dvalid ? d : 0;
   const int lc = cok ? lane : 0;  // channel this thread stages / flushes (0 when out of range)
   const int64_t bk = blockIdx.y;
@@ -500,12 +502,12 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   };
   auto store_tile = [&](int buf, const TileRows& rows, int nt) {
     // the prefetched values are first consumed here, after the tile's math
-    mask_xtile(pu, cok);
-    mask_xtile(pd, cok);
-    mask_xtile(pg, cok);
+    mask_xtile(pu, cok, all_in);
+    mask_xtile(pd, cok, all_in);
+    mask_xtile(pg, cok, all_in);
     if (gate) {
-      mask_xtile(pz, cok);
-      mask_xtile(pyr, cok);
+      mask_xtile(pz, cok, all_in);
+      mask_xtile(pyr, cok, all_in);
     }
     pb = mask_stile(pb, N, tid);
     pc = mask_stile(pc, N, tid);

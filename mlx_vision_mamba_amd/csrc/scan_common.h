@@ -277,9 +277,13 @@ __device__ __forceinline__ void load_rows(float (&v)[4], const T* __restrict__ p
 #pragma unroll
   for (int r = 0; r < 4; ++r) v[r] = to_f32(row_elem(p, rows.r[r], st, lc, lb));
 }
-__device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok) {
+// all_in: every channel of the block is < D (block-uniform), so nothing is
+// masked and the selects are skipped by a scalar branch
+__device__ __forceinline__ void mask_xtile(float (&v)[4], bool cok, bool all_in) {
+  if (!all_in) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = cok ? v[r] : 0.f;
+    for (int r = 0; r < 4; ++r) v[r] = cok ? v[r] : 0.f;
+  }
 }
 
 // LDS row of the state-indexed value a thread stages (row w + 4 (l >> 4)).
@@ -309,7 +313,7 @@ __device__ __forceinline__ float load_state(const T* __restrict__ p, const TileR
   }
 }
 __device__ __forceinline__ float mask_stile(float x, int64_t N, int tid) {
-  return (tid & 15) < N ? x : 0.f;
+  return (N >= kStatePad || (tid & 15) < N) ? x : 0.f;  // uniform test first
 }
 
 __device__ __forceinline__ void store_xtile(float (*s)[kChPerBlock], const float (&v)[4], int tid) {

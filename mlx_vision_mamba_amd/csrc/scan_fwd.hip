@@ -62,6 +62,7 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int64_t dld = ch0 + lane;                          // channel this thread loads / stores
   const bool dvalid = d < gm.D;
   const bool cok = dld < gm.D;
+  const bool all_in = ch0 + kChPerBlock <= gm.D;  // block-uniform: no channel masked
   const int64_t dc = dvalid ? d : 0;
   const int lc = cok ? lane : 0;
   const int64_t bk = blockIdx.y;
@@ -194,8 +195,8 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // zero the out-of-range channels / states of a prefetched tile: the first
   // use of its values, after the current tile's math
   auto mask_tile = [&](float (&pu)[4], float (&pd)[4], float& pb, float& pc) {
-    mask_xtile(pu, cok);
-    mask_xtile(pd, cok);
+    mask_xtile(pu, cok, all_in);
+    mask_xtile(pd, cok, all_in);
     pb = mask_stile(pb, N, tid);
     pc = mask_stile(pc, N, tid);
   };
