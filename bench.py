@@ -11,7 +11,8 @@ batch 32 of 224x224x1 images ~ N(0,1), patch 16 -> 196 tokens, embed_dim
 384 (d_inner 768), d_state 16, depth 6, float32 random-init weights
 (Kaiming-uniform projections, S4D-real A, dt bias with softplus(bias) in
 [1e-3, 1e-1]); loss = mean of the output features; one step = forward +
-loss + backward + AdamW update (torch's fused AdamW).  The fp32 projection
+loss + backward + AdamW update (the package's one-launch AdamW,
+mlx_vision_mamba_amd.optim; --torch-adamw for torch's fused AdamW).  The fp32 projection
 GEMMs use the TunableOp picks recorded for this step on MI355X
 (mlx_vision_mamba_amd/tuning/, read-only; --default-gemms for the library
 defaults).  Inputs are resident on the GPU before the
@@ -93,6 +94,18 @@ def _seeded_model(torch, mvm, device):
     return model.to(device)
 
 
+TORCH_ADAMW = False  # --torch-adamw
+
+
+def _adamw(torch, model, capturable):
+    """The train step's optimiser (lr 1e-4, otherwise AdamW defaults): the
+    package's one-launch AdamW, or torch's fused AdamW with --torch-adamw."""
+    if TORCH_ADAMW:
+        return torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=capturable)
+    from mlx_vision_mamba_amd.optim import AdamW
+    return AdamW(model.parameters(), lr=1e-4)
+
+
 def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     """Time `steps` train steps after `warmup` untimed ones.
 
@@ -110,8 +123,8 @@ def bench_step(torch, mvm, scan, steps, warmup, device, graph=True):
     # the captured step needs a capturable optimizer (its step count lives on
     # the device); the eager region uses the plain fused AdamW, whose host
     # path is the cheaper one
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=graph)
-    opt_eager = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True) if graph else opt
+    opt = _adamw(torch, model, capturable=graph)
+    opt_eager = _adamw(torch, model, capturable=False) if graph else opt
 
     def step(o=opt):
         o.zero_grad(set_to_none=True)
@@ -212,7 +225,7 @@ def bench_encoder(torch, mvm, scan, name, steps, warmup, device):
     model = mvm.VisionMamba(in_channels=1, embed_dim=384, depth=6, d_state=16, scan_mode="hip",
                             **kw).to(device)
     x = torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(device)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=True)
+    opt = _adamw(torch, model, capturable=True)
     side = torch.cuda.Stream(device)
     side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
@@ -236,7 +249,7 @@ def bench_encoder(torch, mvm, scan, name, steps, warmup, device):
     elapsed = time.perf_counter() - t0
     del g
     # eager steps with every scan launch timed on its stream
-    opt_e = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    opt_e = _adamw(torch, model, capturable=False)
     for _ in range(2):
         opt_e.zero_grad(set_to_none=True)
         model(x).mean().backward()
@@ -615,10 +628,15 @@ def main():
                          "B=2 L=196 D=1536 N=16 fp32")
     ap.add_argument("--no-encoders", action="store_true",
                     help="skip the 3D (K=6) and 4D (K=8) encoder steps")
+    ap.add_argument("--torch-adamw", action="store_true",
+                    help="update with torch's fused AdamW instead of the package's one-launch "
+                         "AdamW")
     args = ap.parse_args()
+    global TORCH_ADAMW
+    TORCH_ADAMW = args.torch_adamw
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the selective-scan path is benchmarked on a "
-              "single MI355X (see DESIGN.md for how it would shard); run with --gpus 1.",
+              "single MI355X; run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
@@ -700,6 +718,8 @@ def main():
                    "directions": 4, "parallelism": "single GPU"},
         "gemm_selection": ("TunableOp picks " + os.path.relpath(gemm_tuning.DEFAULT_FILE, ROOT)
                            if tuned else "library default"),
+        "optimizer": ("torch fused AdamW" if TORCH_ADAMW
+                      else "one-launch AdamW (mlx_vision_mamba_amd.optim)"),
         "roofline": roofline,
         "scan": scans,
     }

@@ -77,9 +77,24 @@ class NormDesc(ctypes.Structure):
     ]
 
 
+class AdamwTensor(ctypes.Structure):
+    """Mirror of ``mvm_adamw_tensor`` (include/mvm_optim.h)."""
+
+    _fields_ = [("param", _vp), ("grad", _vp), ("numel", _i64), ("state_offset", _i64)]
+
+
+class AdamwHparams(ctypes.Structure):
+    """Mirror of ``mvm_adamw_hparams`` (include/mvm_optim.h)."""
+
+    _fields_ = [
+        ("lr", ctypes.c_float), ("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+        ("eps", ctypes.c_float), ("weight_decay", ctypes.c_float), ("reserved", _i32),
+    ]
+
+
 # symbol -> (restype, argtypes); every entry point of include/mvm_scan.h,
-# include/mvm_conv.h, include/mvm_norm.h and the test hook of
-# include/mvm_testing.h
+# include/mvm_conv.h, include/mvm_norm.h, include/mvm_optim.h and the test
+# hook of include/mvm_testing.h
 SIGNATURES = {
     "mvm_abi_version": (ctypes.c_int, []),
     "mvm_last_error": (ctypes.c_char_p, []),
@@ -103,6 +118,8 @@ SIGNATURES = {
     "mvm_norm_workspace_bytes": (_i64, [ctypes.POINTER(NormDesc)]),
     "mvm_layernorm_fwd": (ctypes.c_int, [ctypes.POINTER(NormDesc)] + [_vp] * 7),
     "mvm_layernorm_bwd": (ctypes.c_int, [ctypes.POINTER(NormDesc)] + [_vp] * 10 + [ctypes.c_size_t, _vp]),
+    "mvm_adamw_step": (ctypes.c_int, [ctypes.POINTER(AdamwTensor), _i32, ctypes.POINTER(AdamwHparams),
+                                      _vp, _vp, _vp, _vp]),
     "mvm_selftest_lanes": (ctypes.c_int, [_vp, _vp]),
 }
 

@@ -22,7 +22,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libmvm_scan.so")
-SOURCES = ["capi.hip", "scan_fwd.hip", "scan_bwd.hip", "conv.hip", "layernorm.hip"]
+SOURCES = ["capi.hip", "scan_fwd.hip", "scan_bwd.hip", "conv.hip", "layernorm.hip", "optim.hip"]
 ARCH = "gfx950"
 
 

@@ -1,5 +1,5 @@
-// C ABI of libmvm_scan.so (declared in include/mvm_scan.h, mvm_conv.h and
-// mvm_norm.h).
+// C ABI of libmvm_scan.so (declared in include/mvm_scan.h, mvm_conv.h,
+// mvm_norm.h and mvm_optim.h).
 //
 // Host-side responsibilities: validate every argument before anything is
 // enqueued, pick the time-chunk length, carve the caller's workspace into
@@ -17,7 +17,9 @@
 #include "conv_kernels.h"
 #include "mvm_conv.h"
 #include "mvm_norm.h"
+#include "mvm_optim.h"
 #include "norm_kernels.h"
+#include "optim_kernels.h"
 #include "mvm_scan.h"
 #include "mvm_testing.h"
 #include "scan_common.h"
@@ -741,6 +743,71 @@ int mvm_layernorm_bwd(const mvm_norm_desc* desc, const float* x, const float* ga
                                          static_cast<float*>(workspace),
                                          static_cast<hipStream_t>(stream)),
                     "mvm_layernorm_bwd launch");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ AdamW
+
+static_assert(MVM_ADAMW_TENSORS_PER_LAUNCH == mvm::kAdamPerLaunch,
+              "header and kernel agree on the tensors per launch");
+
+extern "C" {
+
+int mvm_adamw_step(const mvm_adamw_tensor* tensors, int32_t ntensors,
+                   const mvm_adamw_hparams* hp, const float* step, float* exp_avg,
+                   float* exp_avg_sq, void* stream) {
+  if (hp == nullptr) return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: hparams is NULL");
+  if (hp->reserved != 0) return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: reserved must be 0");
+  if (!(hp->lr >= 0.f) || !(hp->beta1 >= 0.f && hp->beta1 < 1.f) ||
+      !(hp->beta2 >= 0.f && hp->beta2 < 1.f) || !(hp->eps > 0.f) || !(hp->weight_decay >= 0.f))
+    return fail(MVM_ERR_INVALID_ARG,
+                "mvm_adamw_step: bad hyperparameters (lr=%g beta1=%g beta2=%g eps=%g wd=%g)",
+                hp->lr, hp->beta1, hp->beta2, hp->eps, hp->weight_decay);
+  if (ntensors < 0) return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: ntensors=%d < 0", ntensors);
+  if (ntensors == 0) return ok();
+  if (tensors == nullptr) return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: tensors is NULL");
+  if (!step || !exp_avg || !exp_avg_sq)
+    return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: NULL step or state buffer");
+  for (int32_t i = 0; i < ntensors; ++i) {
+    const mvm_adamw_tensor& t = tensors[i];
+    if (t.numel < 0 || t.state_offset < 0)
+      return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: tensor %d: numel=%lld state_offset=%lld",
+                  i, (long long)t.numel, (long long)t.state_offset);
+    if (t.numel > 0 && (!t.param || !t.grad))
+      return fail(MVM_ERR_INVALID_ARG, "mvm_adamw_step: tensor %d: NULL param or grad", i);
+    if (t.numel > (int64_t{1} << 40))
+      return fail(MVM_ERR_UNSUPPORTED, "mvm_adamw_step: tensor %d: numel=%lld too large", i,
+                  (long long)t.numel);
+  }
+  mvm::AdamLaunch a{};
+  a.lr = hp->lr; a.beta1 = hp->beta1; a.beta2 = hp->beta2; a.eps = hp->eps;
+  a.wd = hp->weight_decay;
+  a.step = step; a.m = exp_avg; a.v = exp_avg_sq;
+  auto flush = [&]() -> int {
+    const int rc = hip_status(mvm::launch_adamw(a, static_cast<hipStream_t>(stream)),
+                              "mvm_adamw_step launch");
+    a.nt = 0;
+    a.nblk = 0;
+    return rc;
+  };
+  for (int32_t i = 0; i < ntensors; ++i) {
+    const mvm_adamw_tensor& t = tensors[i];
+    if (t.numel == 0) continue;
+    const int64_t nb = ceil_div(t.numel, mvm::kAdamElems);
+    if (a.nt == mvm::kAdamPerLaunch || a.nblk + nb > INT32_MAX) {
+      const int rc = flush();
+      if (rc != MVM_OK) return rc;
+    }
+    mvm::AdamSlice& sl = a.t[a.nt++];
+    sl.p = t.param;
+    sl.g = t.grad;
+    sl.n = t.numel;
+    sl.soff = t.state_offset;
+    sl.blk0 = a.nblk;
+    a.nblk += static_cast<int32_t>(nb);
+  }
+  return a.nt > 0 ? flush() : ok();
 }
 
 }  // extern "C"

@@ -19,7 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared_functions():
     names = []
-    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_optim.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(", text)
@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 def _header_arity():
     """Parameter count of every function declared in the headers."""
     out = {}
-    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_testing.h"):
+    for hdr in ("mvm_scan.h", "mvm_conv.h", "mvm_norm.h", "mvm_optim.h", "mvm_testing.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for name, params in re.findall(r"\b(mvm_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
@@ -409,3 +409,47 @@ def test_noalloc_backward_rejects_before_touching_the_gpu():
     step = _desc(B=32, L=196, D=768, N=16, K=4)
     assert 0 < lib.mvm_scan_workspace_bytes(ctypes.byref(step), 1) <= cap
     assert lib.mvm_scan_workspace_bytes(ctypes.byref(d), 1) <= cap
+
+
+def test_adamw_rejects_bad_arguments_on_the_host():
+    """mvm_adamw_step validates its hyperparameters and tensor table before
+    any launch (no GPU needed); an empty table is a no-op."""
+    lib = _lib.lib()
+    fake, null = ctypes.c_void_p(0x1000), ctypes.c_void_p(0)
+
+    def hp(**kw):
+        h = _lib.AdamwHparams()
+        h.lr, h.beta1, h.beta2, h.eps, h.weight_decay, h.reserved = 1e-3, 0.9, 0.999, 1e-8, 0.01, 0
+        for k, v in kw.items():
+            setattr(h, k, v)
+        return h
+
+    tab = (_lib.AdamwTensor * 2)()
+    for t in tab:
+        t.param, t.grad, t.numel, t.state_offset = 0x1000, 0x2000, 10, 0
+    good = hp()
+    assert lib.mvm_adamw_step(tab, 0, ctypes.byref(good), fake, fake, fake, null) == _lib.MVM_OK
+    for bad in (hp(beta1=1.0), hp(beta2=-0.1), hp(eps=0.0), hp(lr=-1.0), hp(weight_decay=-1.0),
+                hp(reserved=1), hp(lr=float("nan"))):
+        assert lib.mvm_adamw_step(tab, 2, ctypes.byref(bad), fake, fake, fake, null) == \
+            _lib.MVM_ERR_INVALID_ARG
+    assert lib.mvm_adamw_step(tab, 2, None, fake, fake, fake, null) == _lib.MVM_ERR_INVALID_ARG
+    assert lib.mvm_adamw_step(tab, -1, ctypes.byref(good), fake, fake, fake, null) == \
+        _lib.MVM_ERR_INVALID_ARG
+    assert lib.mvm_adamw_step(None, 2, ctypes.byref(good), fake, fake, fake, null) == \
+        _lib.MVM_ERR_INVALID_ARG
+    assert lib.mvm_adamw_step(tab, 2, ctypes.byref(good), null, fake, fake, null) == \
+        _lib.MVM_ERR_INVALID_ARG
+    tab[1].numel = -5
+    assert lib.mvm_adamw_step(tab, 2, ctypes.byref(good), fake, fake, fake, null) == \
+        _lib.MVM_ERR_INVALID_ARG
+    tab[1].numel, tab[1].grad = 10, 0
+    assert lib.mvm_adamw_step(tab, 2, ctypes.byref(good), fake, fake, fake, null) == \
+        _lib.MVM_ERR_INVALID_ARG
+    assert "NULL param or grad" in _lib.last_error()
+
+
+def test_adamw_cpu_parameters_raise_no_fallback():
+    from mlx_vision_mamba_amd.optim import AdamW
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        AdamW([torch.nn.Parameter(torch.zeros(3))])
