@@ -175,8 +175,18 @@ conv_reduce_kernel(ConvGeom g, int kc, int64_t nparts, const float* __restrict__
   const int64_t colc = col < ncol ? col : 0;
   const int64_t per = (nparts + 3) / 4;
   const int64_t q0 = wave * per, q1 = min(nparts, q0 + per);
+  // the partials are added in order; each batch's loads are in flight
+  // together (from in-bounds rows), not waited for one at a time
+  constexpr int kBatch = 8;
   double s = 0.0;
-  for (int64_t q = q0; q < q1; ++q) s += part[q * ncol + colc];
+  for (int64_t qb = q0; qb < q1; qb += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = part[(qb + u < q1 ? qb + u : q0) * ncol + colc];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (qb + u < q1) s += v[u];
+  }
   sq[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && col < ncol) {
