@@ -213,11 +213,15 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // stays for the fused softplus gradient); per-wave channel sums of dB | dC
   // (one buffer when lean); lean: each thread's float64 dA (4 states) and dD
   // running sums
-  __shared__ float sU[2][kSub][kChPerBlock];
-  __shared__ float sD[2][kSub][kChPerBlock];
-  __shared__ float sG[2][kSub][kChPerBlock];
-  __shared__ float sB[2][kSub][kStatePad];
-  __shared__ float sC[2][kSub][kStatePad];
+  // one array, so that the three tiles sit at fixed distances: a thread's
+  // accesses to its slot in all three share one address (immediate offsets)
+  __shared__ float sX[3][2][kSub][kChPerBlock];
+  __shared__ float sBC[2][2][kSub][kStatePad];
+  float (*const sU)[kSub][kChPerBlock] = sX[0];
+  float (*const sD)[kSub][kChPerBlock] = sX[1];
+  float (*const sG)[kSub][kChPerBlock] = sX[2];
+  float (*const sB)[kSub][kStatePad] = sBC[0];
+  float (*const sC)[kSub][kStatePad] = sBC[1];
   __shared__ float sRed[kLean ? 1 : 2][4][kSub][2][kStatePad];
   __shared__ double sAcc[5][kLean ? kThreads : 1];
   __shared__ double sDb[4][kChPerBlock];  // fused: per-wave dt_bias gradient sums
