@@ -53,9 +53,10 @@ namespace mvm {
 template <typename XT, bool FUSE, bool TOK, typename IdxT>
 __global__ void __launch_bounds__(kThreads)
 scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
-  __shared__ float sD[2][kSub][kChPerBlock];
-  __shared__ float sG[2][kSub][kChPerBlock];
+  __shared__ float sX[2][2][kSub][kChPerBlock];  // delta, dy: one array (shared addresses)
   __shared__ float sC[2][kSub][kStatePad];
+  float (*const sD)[kSub][kChPerBlock] = sX[0];
+  float (*const sG)[kSub][kChPerBlock] = sX[1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;

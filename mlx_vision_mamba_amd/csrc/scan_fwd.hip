@@ -47,10 +47,14 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   // double-buffered tile staging: u, delta (64 channels), B, C (16 states);
   // y replaces u in place and is written back coalesced one tile later (each
   // thread flushes exactly the LDS slots it refills with the next prefetch)
-  __shared__ float sU[2][kSub][kChPerBlock];
-  __shared__ float sD[2][kSub][kChPerBlock];
-  __shared__ float sB[2][kSub][kStatePad];
-  __shared__ float sC[2][kSub][kStatePad];
+  // (one array per kind, so that a thread's slots in both tiles share one
+  // address and immediate offsets)
+  __shared__ float sX[2][2][kSub][kChPerBlock];
+  __shared__ float sBC[2][2][kSub][kStatePad];
+  float (*const sU)[kSub][kChPerBlock] = sX[0];
+  float (*const sD)[kSub][kChPerBlock] = sX[1];
+  float (*const sB)[kSub][kStatePad] = sBC[0];
+  float (*const sC)[kSub][kStatePad] = sBC[1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
