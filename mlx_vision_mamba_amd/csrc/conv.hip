@@ -22,15 +22,33 @@ namespace mvm {
 constexpr int kCvPos = 16;        // positions per wave
 constexpr int kCvBlockPos = 64;   // positions per block
 
-// Token rows are looked up in uniform control flow (scalar loads through
-// the constant address space) and every row load goes to an in-bounds,
-// clamped address whose value is then selected away when the position or
-// channel is out of range: no load sits behind a divergent branch, so the
-// window's loads issue back to back instead of waiting one by one.
+// Every row load goes to an in-bounds, clamped address whose value is then
+// selected away when the position or channel is out of range: no load sits
+// behind a divergent branch, so the window's loads issue back to back
+// instead of waiting one by one.  A row's address is a scalar base (the
+// token row, read out of lane_rows) plus the lane's 32-bit byte offset, so
+// each load needs one VGPR of address, not two.
+//
+// lane_rows: the token row of position p0 + step * lane (clamped into
+// [0, L)) in each lane.  One vector load fetches the rows of up to 64
+// wave-uniform positions, which row_at then reads out with readlane (into
+// SGPRs), instead of one dependent scalar load per position.
 template <bool TOK>
-__device__ __forceinline__ int64_t safe_row(const int32_t* tok, int64_t p, int64_t L) {
-  return row_of<TOK>(tok, p < 0 ? 0 : (p >= L ? L - 1 : p), L);
+__device__ __forceinline__ int32_t lane_rows(const int32_t* tok, int64_t p0, int step, int lane,
+                                             int64_t L) {
+  const int64_t p = p0 + static_cast<int64_t>(step) * lane;
+  const int64_t pc = p < 0 ? 0 : (p >= L ? L - 1 : p);
+  if constexpr (TOK) {
+    const int32_t r = tok[pc];
+    return r < 0 ? 0 : (r >= L ? static_cast<int32_t>(L - 1) : r);
+  } else {
+    return static_cast<int32_t>(pc);
+  }
 }
+__device__ __forceinline__ int64_t row_at(int32_t rows, int i) {
+  return static_cast<int64_t>(__builtin_amdgcn_readlane(rows, i));
+}
+
 // v, or +0 when the (wave-uniform) position is outside [0, L): a bit mask
 // rather than a select, so the load is not moved under a branch
 __device__ __forceinline__ float keep_if(float v, bool in_range) {
@@ -61,16 +79,18 @@ conv_fwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
                      __builtin_amdgcn_readfirstlane(wave) * kCvPos;
   if (s0 >= g.L) return;
   const int32_t* tok = g.tok ? g.tok + k * g.L : nullptr;
-  const float* xb = x + b * g.xsb + k * g.xsk + dc;
-  float* yb = y + b * g.ysb + k * g.ysk + dc;
+  const float* xs = x + b * g.xsb + k * g.xsk;
+  float* ys = y + b * g.ysb + k * g.ysk;
+  const uint32_t lo = static_cast<uint32_t>(dc) * 4u;  // lane byte offset
   float wv[KC];
 #pragma unroll
   for (int j = 0; j < KC; ++j) wv[j] = w[(k * g.D + dc) * KC + j];
   const float bs = bias[k * g.D + dc];
-  // window: xw[i] = x at position s0 - (KC-1) + i
+  // window: xw[i] = x at position s0 - (KC-1) + i (token row: lane i of rx)
+  const int32_t rx = lane_rows<TOK>(tok, s0 - (KC - 1), 1, lane, g.L);
   float xw[kCvPos + KC - 1];
 #pragma unroll
-  for (int i = 0; i < kCvPos + KC - 1; ++i) xw[i] = xb[safe_row<TOK>(tok, s0 - (KC - 1) + i, g.L) * g.xst];
+  for (int i = 0; i < kCvPos + KC - 1; ++i) xw[i] = *at_bytes(xs + row_at(rx, i) * g.xst, lo);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
 #pragma unroll
   for (int i = 0; i < kCvPos + KC - 1; ++i) {
@@ -81,7 +101,7 @@ conv_fwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
   for (int i = 0; i < kCvPos; ++i) {
     const int64_t p = s0 + i;
     const float pre = conv_at<KC>(wv, xw + i, bs);
-    if (p < g.L && dvalid) yb[row_of<TOK>(tok, p, g.L) * g.yst] = pre * sigmoid_f(pre);
+    if (p < g.L && dvalid) *at_bytes(ys + row_at(rx, i + KC - 1) * g.yst, lo) = pre * sigmoid_f(pre);
   }
 }
 
@@ -92,32 +112,34 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
                 float* __restrict__ dx, float* __restrict__ part) {
   __shared__ float sPart[4][KC + 1][64];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + lane;
   const bool dvalid = d < g.D;
   const int64_t dc = dvalid ? d : 0;
   const int64_t bk = blockIdx.y;
   const int64_t b = bk / g.K, k = bk - (bk / g.K) * g.K;
-  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos +
-                     __builtin_amdgcn_readfirstlane(wave) * kCvPos;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.z) * kCvBlockPos + wave * kCvPos;
   const int32_t* tok = g.tok ? g.tok + k * g.L : nullptr;
-  const float* xb = x + b * g.xsb + k * g.xsk + dc;
-  const float* dyb = dy + b * g.ysb + k * g.ysk + dc;
-  float* dxb = dx + b * g.dxsb + k * g.dxsk + dc;
+  const float* xs = x + b * g.xsb + k * g.xsk;
+  const float* dys = dy + b * g.ysb + k * g.ysk;
+  float* dxs = dx + b * g.dxsb + k * g.dxsk;
+  const uint32_t lo = static_cast<uint32_t>(dc) * 4u;  // lane byte offset
   float wv[KC];
 #pragma unroll
   for (int j = 0; j < KC; ++j) wv[j] = w[(k * g.D + dc) * KC + j];
   const float bs = bias[k * g.D + dc];
-  // x at positions s0 - (KC-1) .. s0 + kCvPos - 1 + (KC-1)
+  // x at positions s0 - (KC-1) .. s0 + kCvPos - 1 + (KC-1) (token row of
+  // position s0 - (KC-1) + i: lane i of rx)
+  const int32_t rx = lane_rows<TOK>(tok, s0 - (KC - 1), 1, lane, g.L);
   constexpr int kXW = kCvPos + 2 * (KC - 1);
   float xw[kXW];
 #pragma unroll
-  for (int i = 0; i < kXW; ++i) xw[i] = xb[safe_row<TOK>(tok, s0 - (KC - 1) + i, g.L) * g.xst];
+  for (int i = 0; i < kXW; ++i) xw[i] = *at_bytes(xs + row_at(rx, i) * g.xst, lo);
   // dpre at positions s0 .. s0 + kCvPos - 1 + (KC-1)
   constexpr int kGW = kCvPos + KC - 1;
   float gp[kGW];
 #pragma unroll
-  for (int i = 0; i < kGW; ++i) gp[i] = dyb[safe_row<TOK>(tok, s0 + i, g.L) * g.yst];
+  for (int i = 0; i < kGW; ++i) gp[i] = *at_bytes(dys + row_at(rx, i + KC - 1) * g.yst, lo);
   __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first use
 #pragma unroll
   for (int i = 0; i < kXW; ++i) {
@@ -142,7 +164,7 @@ conv_bwd_kernel(ConvGeom g, const float* __restrict__ x, const float* __restrict
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < KC; ++j) acc = fmaf(wv[j], gp[i + (KC - 1) - j], acc);
-    if (dvalid && p < g.L) dxb[row_of<TOK>(tok, p, g.L) * g.dxst] = acc;
+    if (dvalid && p < g.L) *at_bytes(dxs + row_at(rx, i + KC - 1) * g.dxst, lo) = acc;
     // dw[j] += dpre[p] * x[p - (KC-1) + j]; db += dpre[p]
 #pragma unroll
     for (int j = 0; j < KC; ++j) dwp[j] = fmaf(gp[i], xw[i + j], dwp[j]);
