@@ -77,3 +77,34 @@ def test_conv_parity(cuda, K, grid, kc):
     assert not dbig[..., din:].any()
     _close(dw, dwr, "dw")
     _close(db, dbr, "dbias")
+
+
+@pytest.mark.parametrize("K,n,kc", [(1, 1, 4), (2, 1, 8), (1, 2, 8), (2, 3, 4), (2, 5, 8), (1, 17, 3)])
+def test_conv_short_sequences(cuda, K, n, kc):
+    """Sequences shorter than the kernel width and than one wave's 16
+    positions: every window reaches before position 0 and past the end, so
+    the clamped token-row loads and the masks carry the result."""
+    from mlx_vision_mamba_amd import directions as dirs
+    from mlx_vision_mamba_amd.conv import causal_conv_silu
+    print(f"case: conv short K={K} n={n} kc={kc}", flush=True)
+    bsz, din = 3, 70
+    gen = torch.Generator().manual_seed(n * 10 + kc)
+    x = torch.randn(bsz, n, K, din, generator=gen)
+    w = torch.randn(K, din, kc, generator=gen) * 0.5
+    b = torch.randn(K, din, generator=gen) * 0.1
+    gy = torch.randn(bsz, n, K, din, generator=gen)
+    tok = dirs.seq_to_tok_table(K, n, None).to(cuda) if K > 1 else None
+    xg = x.to(cuda).requires_grad_(True)
+    wg = w.to(cuda).requires_grad_(True)
+    bg = b.to(cuda).requires_grad_(True)
+    y = causal_conv_silu(xg, wg, bg, tok)
+    dx, dw, db = torch.autograd.grad(y, (xg, wg, bg), gy.to(cuda))
+    xr = x.double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    br = b.double().requires_grad_(True)
+    yr = _ref(xr, wr, br, K, None, kc)
+    dxr, dwr, dbr = torch.autograd.grad(yr, (xr, wr, br), gy.double())
+    _close(y, yr.detach(), "y")
+    _close(dx, dxr, "dx")
+    _close(dw, dwr, "dw")
+    _close(db, dbr, "dbias")
