@@ -82,7 +82,7 @@ extern "C" {
 
 typedef struct mvm_scan_desc {
   int64_t batch;    /* B */
-  int64_t seqlen;   /* L (scan positions per direction) */
+  int64_t seqlen;   /* L (scan positions per direction), <= 2^31 - 65 */
   int64_t dim;      /* D = d_inner, channels */
   int64_t dstate;   /* N, 1..MVM_MAX_DSTATE */
   int64_t ndir;     /* K directions scanned in one call, >= 1 */

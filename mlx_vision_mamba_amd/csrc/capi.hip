@@ -45,6 +45,8 @@ int ok() {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+constexpr int64_t kMaxSeqlen = INT32_MAX - 64;
+
 // Time-chunk length.  One chunk (no carry passes) when the (batch x
 // direction x channel-block) grid alone gives >= 4096 waves (four per SIMD
 // on the 256-CU MI355X); otherwise the sequence is cut until the main passes
@@ -122,7 +124,11 @@ int check_desc(const mvm_scan_desc* d) {
                 (long long)(d->batch * d->ndir));
   if (d->seqlen > 0 && ceil_div(d->seqlen, pick_chunk_len(d)) > 65535)
     return fail(MVM_ERR_UNSUPPORTED, "too many time chunks; raise chunk_len");
-  if (d->seqlen > INT32_MAX) return fail(MVM_ERR_UNSUPPORTED, "seqlen exceeds 2^31-1");
+  // positions are int32 in the kernels, and a tile's rows are formed as
+  // position + up to 63 before they are clamped to seqlen - 1
+  if (d->seqlen > kMaxSeqlen)
+    return fail(MVM_ERR_UNSUPPORTED, "seqlen=%lld exceeds %lld", (long long)d->seqlen,
+                (long long)kMaxSeqlen);
   return MVM_OK;
 }
 

@@ -76,7 +76,8 @@ scan_bwd_agg_kernel(Geom gm, BwdBufs bf) {
   const int32_t L = static_cast<int32_t>(gm.L);
   const int N = static_cast<int>(gm.N);
   const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
-  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
+  // the chunk's end in 64 bits: t0 + chunk_len may pass 2^31 - 1 in the last chunk
+  const int32_t t1 = static_cast<int32_t>(min<int64_t>(gm.L, (chunk + 1) * gm.chunk_len));
   const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
   const float* __restrict__ delta = bf.delta + (b * gm.dsb + k * gm.dsk + ch0);
   const XT* __restrict__ dy = static_cast<const XT*>(bf.dy) + (b * gm.ysb + k * gm.ysk + ch0);
@@ -247,7 +248,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int32_t L = own_sc(static_cast<int32_t>(gm.L));
   const int N = own_sc(static_cast<int>(gm.N));
   const int32_t t0 = own_sc(static_cast<int32_t>(chunk * gm.chunk_len));
-  const int32_t t1 = own_sc(min(L, static_cast<int32_t>(t0 + gm.chunk_len)));
+  // the chunk's end in 64 bits: t0 + chunk_len may pass 2^31 - 1 in the last chunk
+  const int32_t t1 = own_sc(static_cast<int32_t>(min<int64_t>(gm.L, (chunk + 1) * gm.chunk_len)));
   const int32_t* tok = TOK ? own_ptr(gm.tok + k * gm.L) : nullptr;
   // the block's first channel of its (b, k) slab in every tensor, and the
   // row strides in IdxT

@@ -76,7 +76,8 @@ scan_fwd_kernel(Geom gm, FwdBufs bf) {
   const int32_t L = static_cast<int32_t>(gm.L);
   const int N = static_cast<int>(gm.N);
   const int32_t t0 = static_cast<int32_t>(chunk * gm.chunk_len);
-  const int32_t t1 = min(L, static_cast<int32_t>(t0 + gm.chunk_len));
+  // the chunk's end in 64 bits: t0 + chunk_len may pass 2^31 - 1 in the last chunk
+  const int32_t t1 = static_cast<int32_t>(min<int64_t>(gm.L, (chunk + 1) * gm.chunk_len));
   const int32_t* tok = TOK ? gm.tok + k * gm.L : nullptr;
   // the block's first channel of its (b, k) slab in every tensor
   const XT* __restrict__ u = static_cast<const XT*>(bf.u) + (b * gm.xsb + k * gm.xsk + ch0);

@@ -440,8 +440,10 @@ def selective_scan_directions(u, delta, A, B, C, D, seq_to_tok=None, chunk_len=0
     if seq_to_tok is not None:
         if seq_to_tok.dtype != torch.int32 or seq_to_tok.shape != (u.shape[2], u.shape[1]):
             raise ValueError("seq_to_tok must be int32 of shape (K, L)")
-        seq_to_tok = seq_to_tok.to(u.device).contiguous()
+        # checked on the caller's tensor, so that a table kept on the host is
+        # checked once, not again for every fresh device copy
         check_permutation_table(seq_to_tok)
+        seq_to_tok = seq_to_tok.to(u.device).contiguous()
     if forward_only:
         y, _ = scan_forward(u.detach(), delta.detach(), A.detach(), B.detach(), C.detach(),
                             D.detach(), seq_to_tok, _resolve_chunk(u.shape[1], chunk_len), out_dtype)

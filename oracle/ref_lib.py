@@ -34,6 +34,12 @@ def _load():
         lib.oracle_scan_vjp.restype = ctypes.c_int
         lib.oracle_ddelta_scale.argtypes = [i64] * 4 + [fp] * 6 + [dp]
         lib.oracle_ddelta_scale.restype = ctypes.c_int
+        lib.oracle_scan_fwd_f64.argtypes = [i64] * 4 + [dp] * 7
+        lib.oracle_scan_fwd_f64.restype = ctypes.c_int
+        lib.oracle_scan_vjp_f64.argtypes = [i64] * 4 + [dp] * 13
+        lib.oracle_scan_vjp_f64.restype = ctypes.c_int
+        lib.oracle_scan_all.argtypes = [i64] * 4 + [fp] * 7 + [dp] * 8
+        lib.oracle_scan_all.restype = ctypes.c_int
         lib.oracle_num_threads.restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -41,6 +47,10 @@ def _load():
 
 def _f32(x):
     return np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+
+
+def _f64(x):
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float64))
 
 
 def _p(a, ct):
@@ -97,3 +107,50 @@ def ddelta_scale(u, delta, A, B, C, g):
     if rc != 0:
         raise RuntimeError(f"oracle_ddelta_scale failed ({rc})")
     return out
+
+
+def scan_fwd_f64(u, delta, A, B, C, D):
+    """``scan_fwd`` for float64 inputs (the float64 module restatements)."""
+    lib = _load()
+    u, delta, A, B, C, D = map(_f64, (u, delta, A, B, C, D))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    y = np.empty((bsz, L, d), dtype=np.float64)
+    dp = ctypes.c_double
+    rc = lib.oracle_scan_fwd_f64(bsz, L, d, n, *[_p(a, dp) for a in (u, delta, A, B, C, D, y)])
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_fwd_f64 failed ({rc})")
+    return y
+
+
+def scan_vjp_f64(u, delta, A, B, C, D, g):
+    """``scan_vjp`` for float64 inputs."""
+    lib = _load()
+    u, delta, A, B, C, D, g = map(_f64, (u, delta, A, B, C, D, g))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    outs = [np.empty((bsz, L, d)), np.empty((bsz, L, d)), np.empty((d, n)),
+            np.empty((bsz, L, n)), np.empty((bsz, L, n)), np.empty((d,))]
+    dp = ctypes.c_double
+    rc = lib.oracle_scan_vjp_f64(bsz, L, d, n, *[_p(a, dp) for a in (u, delta, A, B, C, D, g)],
+                                 *[_p(o, dp) for o in outs])
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_vjp_f64 failed ({rc})")
+    return tuple(outs)
+
+
+def scan_all(u, delta, A, B, C, D, g):
+    """(y, (du, ddelta, dA, dB, dC, dD), S) in one pass: the results of
+    ``scan_fwd``, ``scan_vjp`` and ``ddelta_scale`` on the same inputs."""
+    lib = _load()
+    u, delta, A, B, C, D, g = map(_f32, (u, delta, A, B, C, D, g))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    outs = [np.empty((bsz, L, d)), np.empty((bsz, L, d)), np.empty((bsz, L, d)), np.empty((d, n)),
+            np.empty((bsz, L, n)), np.empty((bsz, L, n)), np.empty((d,)), np.empty((bsz, L, d))]
+    fp, dp = ctypes.c_float, ctypes.c_double
+    rc = lib.oracle_scan_all(bsz, L, d, n, *[_p(a, fp) for a in (u, delta, A, B, C, D, g)],
+                             *[_p(o, dp) for o in outs])
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_all failed ({rc})")
+    return outs[0], tuple(outs[1:7]), outs[7]

@@ -14,10 +14,13 @@
  *             reductions at :213-224 (dD over b, dA over b and t, dB and dC
  *             over channels).
  *
- * Inputs are float32 (the exact values handed to the GPU), all arithmetic
- * and outputs are float64.  Channels are independent, so the loops run one
- * (b, d) pair at a time and keep only that pair's L x N states.
- * tests/test_oracle.py checks this library against scan_oracle.py.
+ * Inputs are float32 (the exact values handed to the GPU; oracle_scan_fwd,
+ * oracle_scan_vjp, oracle_scan_all) or float64 (the _f64 forms, for the
+ * float64 module restatements), all arithmetic and outputs are float64.
+ * Channels are independent, so the loops run one (b, d) pair at a time and
+ * keep only that pair's L x N states.
+ * tests/test_oracle.py checks this library against scan_oracle.py, and
+ * oracle_scan_all against the three single-purpose functions.
  */
 #include <math.h>
 #include <stdint.h>
@@ -35,114 +38,120 @@ int oracle_num_threads(void) {
 #endif
 }
 
-/* y: (B, L, D) float64. */
-int oracle_scan_fwd(int64_t Bsz, int64_t L, int64_t D, int64_t N,
-                    const float* u, const float* delta, const float* A,
-                    const float* Bm, const float* Cm, const float* Dv,
-                    double* y) {
-  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
-#pragma omp parallel for collapse(2) schedule(static)
-  for (int64_t b = 0; b < Bsz; ++b) {
-    for (int64_t d = 0; d < D; ++d) {
-      double h[64];
-      for (int64_t n = 0; n < N; ++n) h[n] = 0.0;
-      for (int64_t t = 0; t < L; ++t) {
-        const int64_t xi = (b * L + t) * D + d;
-        const int64_t bi = (b * L + t) * N;
-        const double dt = delta[xi], x = u[xi];
-        double acc = 0.0;
-        for (int64_t n = 0; n < N; ++n) {
-          const double e = exp(dt * (double)A[d * N + n]);
-          h[n] = e * h[n] + dt * (double)Bm[bi + n] * x;
-          acc += h[n] * (double)Cm[bi + n];
-        }
-        y[xi] = acc + x * (double)Dv[d];
-      }
-    }
+/* y: (B, L, D) float64.  T is the input element type. */
+#define DEFINE_SCAN_FWD(NAME, T)                                                   \
+  int NAME(int64_t Bsz, int64_t L, int64_t D, int64_t N, const T* u,               \
+           const T* delta, const T* A, const T* Bm, const T* Cm, const T* Dv,      \
+           double* y) {                                                            \
+    if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;                  \
+    _Pragma("omp parallel for collapse(2) schedule(static)")                       \
+    for (int64_t b = 0; b < Bsz; ++b) {                                            \
+      for (int64_t d = 0; d < D; ++d) {                                            \
+        double h[64];                                                              \
+        for (int64_t n = 0; n < N; ++n) h[n] = 0.0;                                \
+        for (int64_t t = 0; t < L; ++t) {                                          \
+          const int64_t xi = (b * L + t) * D + d;                                  \
+          const int64_t bi = (b * L + t) * N;                                      \
+          const double dt = delta[xi], x = u[xi];                                  \
+          double acc = 0.0;                                                        \
+          for (int64_t n = 0; n < N; ++n) {                                        \
+            const double e = exp(dt * (double)A[d * N + n]);                       \
+            h[n] = e * h[n] + dt * (double)Bm[bi + n] * x;                         \
+            acc += h[n] * (double)Cm[bi + n];                                      \
+          }                                                                        \
+          y[xi] = acc + x * (double)Dv[d];                                         \
+        }                                                                          \
+      }                                                                            \
+    }                                                                              \
+    return 0;                                                                      \
   }
-  return 0;
-}
+
+DEFINE_SCAN_FWD(oracle_scan_fwd, float)
+DEFINE_SCAN_FWD(oracle_scan_fwd_f64, double)
 
 /* Reverse-scan VJP.  du, ddelta: (B,L,D); dA: (D,N); dB, dC: (B,L,N);
  * dD: (D).  All float64, fully reduced. */
-int oracle_scan_vjp(int64_t Bsz, int64_t L, int64_t D, int64_t N,
-                    const float* u, const float* delta, const float* A,
-                    const float* Bm, const float* Cm, const float* Dv,
-                    const float* g, double* du, double* ddelta, double* dA,
-                    double* dB, double* dC, double* dD) {
-  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
-  const int64_t nbl = Bsz * L * N;
-  memset(dA, 0, sizeof(double) * (size_t)(D * N));
-  memset(dB, 0, sizeof(double) * (size_t)nbl);
-  memset(dC, 0, sizeof(double) * (size_t)nbl);
-  memset(dD, 0, sizeof(double) * (size_t)D);
-  int fail = 0;
-#pragma omp parallel
-  {
-    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
-    double* lB = (double*)calloc((size_t)nbl, sizeof(double));
-    double* lC = (double*)calloc((size_t)nbl, sizeof(double));
-    double* lA = (double*)calloc((size_t)(D * N), sizeof(double));
-    double* lD = (double*)calloc((size_t)D, sizeof(double));
-    const int ok = hs && lB && lC && lA && lD;
-    if (!ok) {
-#pragma omp atomic write
-      fail = 1;
-    }
-    /* every thread reaches the worksharing loop; one without buffers idles */
-#pragma omp for collapse(2) schedule(static)
-      for (int64_t b = 0; b < Bsz; ++b) {
-        for (int64_t d = 0; d < D; ++d) {
-          if (!ok) continue;
-          /* hs[(t+1)*N + n] = h_t, hs[0..N) = h_{-1} = 0 */
-          for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;
-          for (int64_t t = 0; t < L; ++t) {
-            const int64_t xi = (b * L + t) * D + d;
-            const int64_t bi = (b * L + t) * N;
-            const double dt = delta[xi], x = u[xi];
-            for (int64_t n = 0; n < N; ++n) {
-              const double e = exp(dt * (double)A[d * N + n]);
-              hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x;
-            }
-          }
-          double lam[64];
-          for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;
-          double dDacc = 0.0;
-          for (int64_t t = L - 1; t >= 0; --t) {
-            const int64_t xi = (b * L + t) * D + d;
-            const int64_t bi = (b * L + t) * N;
-            const double dt = delta[xi], x = u[xi], gy = g[xi];
-            dDacc += gy * x;
-            double sdu = 0.0, sdd = 0.0;
-            for (int64_t n = 0; n < N; ++n) {
-              const double a = A[d * N + n];
-              const double e = exp(dt * a);
-              const double bv = Bm[bi + n];
-              const double hp = hs[t * N + n];
-              lam[n] += (double)Cm[bi + n] * gy;
-              sdd += lam[n] * (hp * a * e + bv * x);
-              lA[d * N + n] += lam[n] * hp * dt * e;
-              lB[bi + n] += lam[n] * dt * x;
-              lC[bi + n] += gy * hs[(t + 1) * N + n];
-              sdu += lam[n] * dt * bv;
-              lam[n] *= e;
-            }
-            du[xi] = gy * (double)Dv[d] + sdu;
-            ddelta[xi] = sdd;
-          }
-          lD[d] += dDacc;
-        }
-      }
-#pragma omp critical
-      if (ok) {
-        for (int64_t i = 0; i < nbl; ++i) { dB[i] += lB[i]; dC[i] += lC[i]; }
-        for (int64_t i = 0; i < D * N; ++i) dA[i] += lA[i];
-        for (int64_t i = 0; i < D; ++i) dD[i] += lD[i];
-      }
-    free(hs); free(lB); free(lC); free(lA); free(lD);
+#define DEFINE_SCAN_VJP(NAME, T)                                                   \
+  int NAME(int64_t Bsz, int64_t L, int64_t D, int64_t N, const T* u,               \
+           const T* delta, const T* A, const T* Bm, const T* Cm, const T* Dv,      \
+           const T* g, double* du, double* ddelta, double* dA, double* dB,         \
+           double* dC, double* dD) {                                               \
+    if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;                  \
+    const int64_t nbl = Bsz * L * N;                                               \
+    memset(dA, 0, sizeof(double) * (size_t)(D * N));                               \
+    memset(dB, 0, sizeof(double) * (size_t)nbl);                                   \
+    memset(dC, 0, sizeof(double) * (size_t)nbl);                                   \
+    memset(dD, 0, sizeof(double) * (size_t)D);                                     \
+    int fail = 0;                                                                  \
+    _Pragma("omp parallel")                                                        \
+    {                                                                              \
+      double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));        \
+      double* lB = (double*)calloc((size_t)nbl, sizeof(double));                   \
+      double* lC = (double*)calloc((size_t)nbl, sizeof(double));                   \
+      double* lA = (double*)calloc((size_t)(D * N), sizeof(double));               \
+      double* lD = (double*)calloc((size_t)D, sizeof(double));                     \
+      const int ok = hs && lB && lC && lA && lD;                                   \
+      if (!ok) {                                                                   \
+        _Pragma("omp atomic write")                                                \
+        fail = 1;                                                                  \
+      }                                                                            \
+      /* every thread reaches the worksharing loop; one without buffers idles */  \
+      _Pragma("omp for collapse(2) schedule(static)")                              \
+      for (int64_t b = 0; b < Bsz; ++b) {                                          \
+        for (int64_t d = 0; d < D; ++d) {                                          \
+          if (!ok) continue;                                                       \
+          /* hs[(t+1)*N + n] = h_t, hs[0..N) = h_{-1} = 0 */                       \
+          for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;                             \
+          for (int64_t t = 0; t < L; ++t) {                                        \
+            const int64_t xi = (b * L + t) * D + d;                                \
+            const int64_t bi = (b * L + t) * N;                                    \
+            const double dt = delta[xi], x = u[xi];                                \
+            for (int64_t n = 0; n < N; ++n) {                                      \
+              const double e = exp(dt * (double)A[d * N + n]);                     \
+              hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x; \
+            }                                                                      \
+          }                                                                        \
+          double lam[64];                                                          \
+          for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;                            \
+          double dDacc = 0.0;                                                      \
+          for (int64_t t = L - 1; t >= 0; --t) {                                   \
+            const int64_t xi = (b * L + t) * D + d;                                \
+            const int64_t bi = (b * L + t) * N;                                    \
+            const double dt = delta[xi], x = u[xi], gy = g[xi];                    \
+            dDacc += gy * x;                                                       \
+            double sdu = 0.0, sdd = 0.0;                                           \
+            for (int64_t n = 0; n < N; ++n) {                                      \
+              const double a = A[d * N + n];                                       \
+              const double e = exp(dt * a);                                        \
+              const double bv = Bm[bi + n];                                        \
+              const double hp = hs[t * N + n];                                     \
+              lam[n] += (double)Cm[bi + n] * gy;                                   \
+              sdd += lam[n] * (hp * a * e + bv * x);                               \
+              lA[d * N + n] += lam[n] * hp * dt * e;                               \
+              lB[bi + n] += lam[n] * dt * x;                                       \
+              lC[bi + n] += gy * hs[(t + 1) * N + n];                              \
+              sdu += lam[n] * dt * bv;                                             \
+              lam[n] *= e;                                                         \
+            }                                                                      \
+            du[xi] = gy * (double)Dv[d] + sdu;                                     \
+            ddelta[xi] = sdd;                                                      \
+          }                                                                        \
+          lD[d] += dDacc;                                                          \
+        }                                                                          \
+      }                                                                            \
+      _Pragma("omp critical")                                                      \
+      if (ok) {                                                                    \
+        for (int64_t i = 0; i < nbl; ++i) { dB[i] += lB[i]; dC[i] += lC[i]; }      \
+        for (int64_t i = 0; i < D * N; ++i) dA[i] += lA[i];                        \
+        for (int64_t i = 0; i < D; ++i) dD[i] += lD[i];                            \
+      }                                                                            \
+      free(hs); free(lB); free(lC); free(lA); free(lD);                            \
+    }                                                                              \
+    return fail ? -2 : 0;                                                          \
   }
-  return fail ? -2 : 0;
-}
+
+DEFINE_SCAN_VJP(oracle_scan_vjp, float)
+DEFINE_SCAN_VJP(oracle_scan_vjp_f64, double)
 
 /* Cancellation scale of ddelta: S[b,t,d] = sum_n |lam_n| * (|A_n e_n h_{t-1,n}|
  * + |B_n u_t|), the sum of the absolute values of the terms whose signed sum
@@ -198,6 +207,95 @@ int oracle_ddelta_scale(int64_t Bsz, int64_t L, int64_t D, int64_t N,
       }
     }
     free(hs);
+  }
+  return fail ? -2 : 0;
+}
+
+/* Forward, VJP and the ddelta scale in one pass per (b, d) pair, for the
+ * parity checks at full size: the same expressions, in the same order, as
+ * oracle_scan_fwd, oracle_scan_vjp and oracle_ddelta_scale, so the results
+ * equal theirs up to the order in which the threads' float64 partial sums
+ * of dA, dB, dC and dD are added (tests/test_oracle.py).  Outputs as in
+ * those three functions. */
+int oracle_scan_all(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                    const float* u, const float* delta, const float* A,
+                    const float* Bm, const float* Cm, const float* Dv,
+                    const float* g, double* y, double* du, double* ddelta,
+                    double* dA, double* dB, double* dC, double* dD,
+                    double* scale) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+  const int64_t nbl = Bsz * L * N;
+  memset(dA, 0, sizeof(double) * (size_t)(D * N));
+  memset(dB, 0, sizeof(double) * (size_t)nbl);
+  memset(dC, 0, sizeof(double) * (size_t)nbl);
+  memset(dD, 0, sizeof(double) * (size_t)D);
+  int fail = 0;
+#pragma omp parallel
+  {
+    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    double* lB = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lC = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lA = (double*)calloc((size_t)(D * N), sizeof(double));
+    double* lD = (double*)calloc((size_t)D, sizeof(double));
+    const int ok = hs && lB && lC && lA && lD;
+    if (!ok) {
+#pragma omp atomic write
+      fail = 1;
+    }
+#pragma omp for collapse(2) schedule(static)
+    for (int64_t b = 0; b < Bsz; ++b) {
+      for (int64_t d = 0; d < D; ++d) {
+        if (!ok) continue;
+        for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;
+        for (int64_t t = 0; t < L; ++t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi];
+          double acc = 0.0;
+          for (int64_t n = 0; n < N; ++n) {
+            const double e = exp(dt * (double)A[d * N + n]);
+            hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x;
+            acc += hs[(t + 1) * N + n] * (double)Cm[bi + n];
+          }
+          y[xi] = acc + x * (double)Dv[d];
+        }
+        double lam[64];
+        for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;
+        double dDacc = 0.0;
+        for (int64_t t = L - 1; t >= 0; --t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi], gy = g[xi];
+          dDacc += gy * x;
+          double sdu = 0.0, sdd = 0.0, s = 0.0;
+          for (int64_t n = 0; n < N; ++n) {
+            const double a = A[d * N + n];
+            const double e = exp(dt * a);
+            const double bv = Bm[bi + n];
+            const double hp = hs[t * N + n];
+            lam[n] += (double)Cm[bi + n] * gy;
+            sdd += lam[n] * (hp * a * e + bv * x);
+            s += fabs(lam[n]) * (fabs(a * e * hp) + fabs(bv * x));
+            lA[d * N + n] += lam[n] * hp * dt * e;
+            lB[bi + n] += lam[n] * dt * x;
+            lC[bi + n] += gy * hs[(t + 1) * N + n];
+            sdu += lam[n] * dt * bv;
+            lam[n] *= e;
+          }
+          du[xi] = gy * (double)Dv[d] + sdu;
+          ddelta[xi] = sdd;
+          scale[xi] = s;
+        }
+        lD[d] += dDacc;
+      }
+    }
+#pragma omp critical
+    if (ok) {
+      for (int64_t i = 0; i < nbl; ++i) { dB[i] += lB[i]; dC[i] += lC[i]; }
+      for (int64_t i = 0; i < D * N; ++i) dA[i] += lA[i];
+      for (int64_t i = 0; i < D; ++i) dD[i] += lD[i];
+    }
+    free(hs); free(lB); free(lC); free(lA); free(lD);
   }
   return fail ? -2 : 0;
 }

@@ -28,6 +28,8 @@ import math
 import torch
 import torch.nn.functional as F
 
+from . import ref_lib
+
 
 # ---------------------------------------------------------------------------
 # Scan modes
@@ -75,6 +77,35 @@ def scan_chunked(x, delta, A, B, C, D, chunk_size=32):
     return torch.cat(parts, dim=1) + x * D                # :73-74
 
 
+class _OracleScanFn(torch.autograd.Function):
+    """The float64 C oracle (scan_ref.c, float64-input forms) as a torch op:
+    forward mamba_block.py:45-74, VJP mamba_metal_fused.py:66-145,
+    213-224.  Same function and gradients as ``scan_sequential`` (checked
+    in tests/test_oracle_blocks.py), without a Python step per position, so
+    the module restatements run at full sequence lengths in seconds."""
+
+    @staticmethod
+    def forward(ctx, x, delta, A, B, C, D):
+        ctx.save_for_backward(x, delta, A, B, C, D)
+        arrs = [t.detach().numpy() for t in (x, delta, A, B, C, D)]
+        return torch.from_numpy(ref_lib.scan_fwd_f64(*arrs))
+
+    @staticmethod
+    def backward(ctx, gy):
+        arrs = [t.detach().numpy() for t in ctx.saved_tensors]
+        grads = ref_lib.scan_vjp_f64(*arrs, gy.detach().double().numpy())
+        return tuple(torch.from_numpy(g) for g in grads)
+
+
+def scan_oracle_c(x, delta, A, B, C, D):
+    """float64 CPU scan with autograd through the C oracle; a drop-in for
+    ``scan_sequential`` in the module restatements (float64 tensors)."""
+    for t in (x, delta, A, B, C, D):
+        if t.dtype != torch.float64 or t.device.type != "cpu":
+            raise ValueError("scan_oracle_c takes float64 CPU tensors")
+    return _OracleScanFn.apply(x, delta, A, B, C, D)
+
+
 # ---------------------------------------------------------------------------
 # Module restatements (float64 by default)
 # ---------------------------------------------------------------------------
@@ -104,9 +135,12 @@ def mamba_block(params, prefix, x, d_state, d_conv, scan=scan_sequential):
     xz = x @ W_in.T                                            # :165
     xb, z = xz[..., :d_inner], xz[..., d_inner:]               # :166-167
     # MLX Conv1d with padding d_conv-1 on both sides, then keep the first L
-    # outputs (:129-132, :170): output t sees inputs t-d_conv+1 .. t.
-    xc = F.conv1d(xb.transpose(1, 2), conv_w, conv_b, padding=d_conv - 1,
-                  groups=d_inner)[..., :L].transpose(1, 2)
+    # outputs (:129-132, :170): output t sees inputs t-d_conv+1 .. t, tap j
+    # weighting input t - (d_conv - 1) + j (a cross-correlation), written
+    # as a sum over the taps of the zero-padded sequence
+    xp = F.pad(xb, (0, 0, d_conv - 1, 0))
+    w = conv_w[:, 0, :]
+    xc = conv_b + sum(xp[:, j:j + L] * w[:, j] for j in range(d_conv))
     xc = xc * torch.sigmoid(xc)                                # :171 SiLU
     dbc = xc @ W_x.T                                           # :174
     dt = dbc[..., :dt_rank]                                    # :175

@@ -48,6 +48,22 @@ def _header_arity():
     return out
 
 
+def test_seqlen_limit_leaves_room_for_tile_rows():
+    """Kernel positions are int32 and a tile's rows are formed as position +
+    up to 63 before they are clamped, so seqlen is capped at 2^31 - 65; the
+    last chunk's end is formed in 64 bits, so a chunk_len that reaches past
+    2^31 - 1 is accepted."""
+    limit = 2 ** 31 - 65
+    d = _desc(B=1, L=limit, D=1, N=1)
+    d.x_stride_b, d.x_stride_t, d.bc_stride_b, d.bc_stride_t = limit, 1, limit, 1
+    d.chunk_len = 2 ** 30
+    assert _validate(d) == 0
+    d.seqlen = limit + 1
+    d.x_stride_b = d.bc_stride_b = limit + 1
+    assert _validate(d) == _lib.MVM_ERR_UNSUPPORTED
+    assert b"seqlen" in _lib.lib().mvm_last_error()
+
+
 def test_ctypes_signatures_match_header_arity():
     arity = _header_arity()
     assert set(arity) == set(_lib.SIGNATURES)

@@ -158,14 +158,21 @@ def test_malformed_direction_table_rejected(cuda):
         mvm.selective_scan_directions(u, u.abs(), A, Bm, Bm, Dv, seq_to_tok=good)
 
 
-@pytest.mark.parametrize("K,grid,bsz", [(4, (14, 14), 2), (8, (8, 4, 4, 4), 1)])
+@pytest.mark.parametrize("K,grid,bsz", [(4, (14, 14), 2), (6, (16, 16, 16), 1), (8, (8, 4, 4, 4), 1)])
 def test_direction_block_at_layer_width(cuda, K, grid, bsz):
     """One encoder layer at its real width (E=384, d_inner=768, N=16):
-    the VisionMamba-2D layer (K=4, 14x14 grid) and the 4D layer (K=8,
-    grid (8, 4, 4, 4), L=512), output and every gradient against the
-    float64 restatement (mamba_block.py:407-566)."""
+    the VisionMamba-2D layer (K=4, 14x14 grid), the 3D layer (K=6, 16^3
+    grid, L=4096: at batch 1 the fused scan runs 52 time chunks of 80
+    positions, joined by the separate carry kernels) and the 4D layer (K=8, grid (8, 4, 4, 4), L=512), output and
+    every gradient against the float64 restatement (mamba_block.py:407-566;
+    its scan is the float64 C oracle, torch_ref.scan_oracle_c)."""
+    from mlx_vision_mamba_amd import scan
     print(f"case: direction block E=384 K={K} grid={grid} batch={bsz}", flush=True)
+    L = int(np.prod(grid))
+    if K == 6:
+        assert -(-L // scan.chunk_len_for(bsz * K, L, 768)) > 8   # the carry kernels run
     torch.manual_seed(5 + K)
     blk = mvm.MultiDirectionalMambaBlock(d_model=384, num_directions=K, grid_shape=grid)
-    x = torch.randn(bsz, int(np.prod(grid)), 384)
-    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4), cuda)
+    x = torch.randn(bsz, L, 384)
+    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4,
+                                                              scan=torch_ref.scan_oracle_c), cuda)

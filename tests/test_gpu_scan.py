@@ -215,13 +215,61 @@ def test_direction_remap_parity(cuda, K, grid):
             assert_close(got, ref, f"{name}[k={k}]", scale=scale if name == "ddelta" else None)
 
 
-def test_parity_long_sequence_shard_bf16(cuda):
-    """B=8, L=16384, N=16 with bf16 u/B/C on a 192-channel slice (one
-    eighth of d_inner=1536), fp32 outputs against the oracle on the same
-    bf16-rounded values."""
-    print("case: B=8 L=16384 D=192 bf16 in fp32 out", flush=True)
-    inputs = scan_inputs.make(8, 16384, 192, 16, seed=11, dtype=torch.bfloat16)
-    check_all(inputs, cuda, out_dtype=torch.float32, raw=True)
+def _host(t):
+    return t.detach().float().cpu().numpy()
+
+
+def test_parity_long_sequence_full_width(cuda):
+    """B=8, L=16384, D=1536, N=16 with bf16 u/B/C/dy and automatic chunking
+    (22 chunks of 752 positions: both aggregate passes and both carry
+    kernels), against the oracle at full width, for both output
+    instantiations: float32 outputs at the scan bar, bf16 outputs
+    (y, du, dB, dC) at the bf16 bar.
+
+    The oracle runs over channel slabs of 192 (each slab a complete
+    oracle call).  y, du, ddelta, dA and dD are compared per slab; dB and dC
+    are sums over all 1536 channels, so they are compared once, against
+    the float64 sum of the slabs' dB and dC: the reduction over the 24
+    channel blocks of the kernels is checked whole."""
+    from mlx_vision_mamba_amd import scan
+    bsz, L, D, N = 8, 16384, 1536, 16
+    assert scan.chunk_len_for(bsz, L, D, N) == 752
+    print("case: B=8 L=16384 D=1536 N=16 bf16 in, fp32 and bf16 out, full width", flush=True)
+    inputs = scan_inputs.make(bsz, L, D, N, seed=11, dtype=torch.bfloat16)
+    gpu = {}
+    for name, odt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        y, grads = run_raw(inputs, cuda, out_dtype=odt)
+        assert y.dtype == odt and grads[0].dtype == odt and grads[3].dtype == odt
+        assert grads[1].dtype == torch.float32 and grads[2].dtype == torch.float32
+        gpu[name] = [_host(y)] + [_host(g) for g in grads]
+        del y, grads
+    torch.cuda.empty_cache()
+    bars = {"f32": {n: (ATOL, RTOL) for n in ("y",) + NAMES},
+            "bf16": {n: ((1e-3, 8e-3) if n in ("y", "du", "dB", "dC") else (ATOL, RTOL))
+                     for n in ("y",) + NAMES}}
+    u, dl, A, Bm, Cm, Dv, g = [t.float().numpy() for t in inputs]
+    dB_ref = np.zeros((bsz, L, N))
+    dC_ref = np.zeros((bsz, L, N))
+    slab = 192
+    for d0 in range(0, D, slab):
+        sl = slice(d0, d0 + slab)
+        cut = [np.ascontiguousarray(x[..., sl]) for x in (u, dl)]
+        y_ref, (du, ddl, dA, dB, dC, dD), S = ref_lib.scan_all(
+            cut[0], cut[1], A[sl], Bm, Cm, Dv[sl], np.ascontiguousarray(g[..., sl]))
+        dB_ref += dB
+        dC_ref += dC
+        for name, got in gpu.items():
+            for key, idx, ref in (("y", 0, y_ref), ("du", 1, du), ("ddelta", 2, ddl)):
+                a, r = bars[name][key]
+                assert_close(torch.from_numpy(got[idx][..., sl]), ref, f"{name} {key} [{d0}:]", a, r,
+                             scale=S if key == "ddelta" else None)
+            assert_close(torch.from_numpy(got[3][sl]), dA, f"{name} dA [{d0}:]")
+            assert_close(torch.from_numpy(got[6][sl]), dD, f"{name} dD [{d0}:]")
+        print(f"slab {d0}:{d0 + slab} ok", flush=True)
+    for name, got in gpu.items():
+        for key, idx, ref in (("dB", 4, dB_ref), ("dC", 5, dC_ref)):
+            a, r = bars[name][key]
+            assert_close(torch.from_numpy(got[idx]), ref, f"{name} {key}", a, r)
 
 
 def test_full_long_sequence_properties(cuda):

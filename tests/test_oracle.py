@@ -223,6 +223,33 @@ def test_c_oracle_matches_numpy(shape, a_mode):
         np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
 
 
+def test_c_oracle_float64_inputs_match_numpy():
+    """The float64-input forms (for the float64 module restatements) on
+    values that float32 cannot hold, against the numpy float64 oracle."""
+    *args, g = _rand(2, 41, 6, 16, seed=15, a_mode="random")
+    args = [np.asarray(a, np.float64) * (1 + 1e-9) for a in args]
+    g = np.asarray(g, np.float64)
+    np.testing.assert_allclose(ref_lib.scan_fwd_f64(*args), so.scan_fwd(*args), rtol=1e-12, atol=1e-13)
+    for a, b in zip(ref_lib.scan_vjp_f64(*args, g), so.scan_vjp(*args, g)):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+    # and equal to the float32-input forms where the values are float32
+    f32 = [a.astype(np.float32) for a in args + [g]]
+    np.testing.assert_array_equal(ref_lib.scan_fwd_f64(*f32[:6]), ref_lib.scan_fwd(*f32[:6]))
+
+
+def test_c_oracle_single_pass_equals_the_three_functions():
+    """oracle_scan_all (the full-size parity checks) returns what
+    scan_fwd, scan_vjp and ddelta_scale return on the same inputs."""
+    *args, g = _rand(3, 57, 9, 16, seed=16, a_mode="random")
+    f32 = [a.astype(np.float32) for a in args + [g]]
+    y, grads, S = ref_lib.scan_all(*f32)
+    np.testing.assert_array_equal(y, ref_lib.scan_fwd(*f32[:6]))
+    for a, b in zip(grads, ref_lib.scan_vjp(*f32)):
+        np.testing.assert_allclose(a, b, rtol=1e-13, atol=1e-15)
+    np.testing.assert_array_equal(grads[0], ref_lib.scan_vjp(*f32)[0])   # per-(b, d): no reduction
+    np.testing.assert_array_equal(S, ref_lib.ddelta_scale(*f32[:5], f32[6]))
+
+
 def test_c_oracle_rejects_bad_state_size():
     *args, g = _rand(1, 3, 2, 4, seed=14)
     bad = [a.astype(np.float32) for a in args]

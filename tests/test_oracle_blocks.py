@@ -302,3 +302,26 @@ def test_vision_mamba_closed_form(input_dim):
     tok = _direction_np(p, "blocks.0.", tok, K, grid)
     ref = _ln(tok, _np(p["norm.weight"]), _np(p["norm.bias"]))
     np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-11)
+
+
+@pytest.mark.parametrize("K,grid", [(4, (3, 5)), (6, (2, 3, 4))])
+def test_c_oracle_scan_op_equals_the_sequential_restatement(K, grid):
+    """torch_ref.scan_oracle_c (the float64 C oracle as a torch op, used
+    by the full-size module checks) gives the same block output and
+    gradients as the op-for-op sequential restatement."""
+    torch.manual_seed(40 + K)
+    blk = mb.MultiDirectionalMambaBlock(d_model=16, num_directions=K, grid_shape=grid)
+    x = torch.randn(2, int(np.prod(grid)), 16, dtype=torch.float64)
+    gy = torch.randn(2, int(np.prod(grid)), 16, dtype=torch.float64)
+    res = []
+    for scan in (torch_ref.scan_sequential, torch_ref.scan_oracle_c):
+        p = torch_ref.params_from_module(blk)
+        xr = x.clone().requires_grad_(True)
+        y = torch_ref.direction_block(p, "", xr, K, grid, 16, 4, scan=scan)
+        y.backward(gy)
+        res.append([y.detach(), xr.grad] + [p[k].grad for k in sorted(p)])
+    for a, b in zip(*res):
+        np.testing.assert_allclose(_np(a), _np(b), rtol=1e-10, atol=1e-12)
+    with pytest.raises(ValueError):
+        torch_ref.scan_oracle_c(*[torch.zeros(1, 2, 3)] * 2, torch.zeros(3, 4),
+                                *[torch.zeros(1, 2, 4)] * 2, torch.zeros(3))
