@@ -40,6 +40,10 @@ def _load():
         lib.oracle_scan_vjp_f64.restype = ctypes.c_int
         lib.oracle_scan_all.argtypes = [i64] * 4 + [fp] * 7 + [dp] * 8
         lib.oracle_scan_all.restype = ctypes.c_int
+        lib.oracle_scan_mag_fwd.argtypes = [i64] * 4 + [dp] * 13
+        lib.oracle_scan_mag_fwd.restype = ctypes.c_int
+        lib.oracle_scan_mag_vjp.argtypes = [i64] * 4 + [dp] * 20
+        lib.oracle_scan_mag_vjp.restype = ctypes.c_int
         lib.oracle_num_threads.restype = ctypes.c_int
         _lib = lib
     return _lib
@@ -154,3 +158,44 @@ def scan_all(u, delta, A, B, C, D, g):
     if rc != 0:
         raise RuntimeError(f"oracle_scan_all failed ({rc})")
     return outs[0], tuple(outs[1:7]), outs[7]
+
+
+def scan_mag_fwd(values, mags):
+    """Error-magnitude companion of the scan forward (scan_ref.c
+    oracle_scan_mag_fwd).  values = (u, delta, A, B, C, D), mags = (Mu, Md,
+    MA, MB, MC, MD), float64 with the shapes of the scan's inputs; returns
+    My (B, L, D)."""
+    lib = _load()
+    vals = list(map(_f64, values))
+    ms = list(map(_f64, mags))
+    bsz, L, d = vals[0].shape
+    n = vals[2].shape[1]
+    for v, m in zip(vals, ms):
+        if v.shape != m.shape:
+            raise ValueError(f"magnitude shape {m.shape} != value shape {v.shape}")
+    out = np.empty((bsz, L, d))
+    dp = ctypes.c_double
+    rc = lib.oracle_scan_mag_fwd(bsz, L, d, n, *[_p(a, dp) for a in vals + ms], _p(out, dp))
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_mag_fwd failed ({rc})")
+    return out
+
+
+def scan_mag_vjp(values, mags, g, Mg):
+    """Error magnitudes of the scan's six gradients (du, ddelta, dA, dB, dC,
+    dD) for the actual cotangent g of y and its magnitude Mg (scan_ref.c
+    oracle_scan_mag_vjp)."""
+    lib = _load()
+    vals = list(map(_f64, values))
+    ms = list(map(_f64, mags))
+    g, Mg = _f64(g), _f64(Mg)
+    bsz, L, d = vals[0].shape
+    n = vals[2].shape[1]
+    outs = [np.empty((bsz, L, d)), np.empty((bsz, L, d)), np.empty((d, n)),
+            np.empty((bsz, L, n)), np.empty((bsz, L, n)), np.empty((d,))]
+    dp = ctypes.c_double
+    rc = lib.oracle_scan_mag_vjp(bsz, L, d, n, *[_p(a, dp) for a in vals + ms + [g, Mg]],
+                                 *[_p(o, dp) for o in outs])
+    if rc != 0:
+        raise RuntimeError(f"oracle_scan_mag_vjp failed ({rc})")
+    return tuple(outs)

@@ -299,3 +299,168 @@ int oracle_scan_all(int64_t Bsz, int64_t L, int64_t D, int64_t N,
   }
   return fail ? -2 : 0;
 }
+
+/* ------------------------------------------------------------------------
+ * Error-magnitude companion of the scan, for the per-element bounds of the
+ * module parity tests (a first-order running error analysis).  Magnitudes
+ * M(x) are in units of 2^-24: a float32 evaluation of x is expected within
+ * a small multiple of 2^-24 M(x) of the exact value, and M(x) >= |x| (each
+ * operation's own rounding).  e = exp(delta A), h the scan's states.
+ *
+ * Forward (mamba_block.py:45-74), given the input magnitudes Mu, Md, MA,
+ * MB, MC, MD:
+ *   H_t  = e_t H_{t-1} + delta_t (MB_t |u_t| + |B_t| Mu_t)
+ *          + Md_t (|A| e_t |h_{t-1}| + |B_t u_t|) + MA delta_t e_t |h_{t-1}|
+ *   My_t = sum_n (|C_t| H_t + MC_t |h_t|) + |D| Mu_t + MD |u_t|
+ * (H_{-1} = 0; H >= |h| when Mu >= |u| and MB >= |B|), linear in the
+ * magnitudes with the values as coefficients.
+ *
+ * Backward (mamba_metal_fused.py:66-145), given the actual cotangent g of y
+ * and its magnitude Mg (>= |g|), with lam the actual adjoint
+ * (lam_t = C_t g_t + e_{t+1} lam_{t+1}) and Me = e (1 + |A| Md + delta MA)
+ * the magnitude of e:
+ *   lM_t  = |C_t| Mg_t + MC_t |g_t| + e_{t+1} lM_{t+1} + Me_{t+1} |lam_{t+1}|
+ *   M(du)     = |D| Mg + MD |g| + sum_n (delta |B| lM + (Md |B| + delta MB) |lam|)
+ *   M(ddelta) = sum_n (lM (|A| e |h_{t-1}| + |B u|) + |lam| (MA e |h_{t-1}|
+ *               + |A| Me |h_{t-1}| + |A| e H_{t-1} + MB |u| + |B| Mu))
+ *   M(dA)     = sum_{b,t} (lM delta e |h_{t-1}| + |lam| (Md e |h_{t-1}|
+ *               + delta Me |h_{t-1}| + delta e H_{t-1}))
+ *   M(dB)     = sum_d (lM delta |u| + |lam| (Md |u| + delta Mu))
+ *   M(dC)     = sum_d (Mg |h_t| + |g| H_t)
+ *   M(dD)     = sum_{b,t} (Mg |u| + |g| Mu)
+ * every term one magnitude times values: each gradient's terms with the
+ * errors of their factors.  Pinned in tests/test_oracle.py: the forward
+ * reduces to oracle_scan_fwd on absolute values; it bounds the finite
+ * differences of the scan in delta and in A; every magnitude is at least
+ * the absolute value it stands for; the scan's own algorithm evaluated in
+ * float32 stays within 2 * 2^-24 * M of the float64 values.
+ * ------------------------------------------------------------------------ */
+int oracle_scan_mag_fwd(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                        const double* u, const double* delta, const double* A,
+                        const double* Bm, const double* Cm, const double* Dv,
+                        const double* Mu, const double* Md, const double* MA,
+                        const double* MB, const double* MC, const double* MD,
+                        double* My) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < Bsz; ++b) {
+    for (int64_t d = 0; d < D; ++d) {
+      double h[64], H[64];
+      for (int64_t n = 0; n < N; ++n) h[n] = H[n] = 0.0;
+      for (int64_t t = 0; t < L; ++t) {
+        const int64_t xi = (b * L + t) * D + d;
+        const int64_t bi = (b * L + t) * N;
+        const double dt = delta[xi], x = u[xi];
+        double acc = 0.0;
+        for (int64_t n = 0; n < N; ++n) {
+          const double a = A[d * N + n];
+          const double e = exp(dt * a);
+          const double bv = Bm[bi + n];
+          H[n] = e * H[n] + dt * (MB[bi + n] * fabs(x) + fabs(bv) * Mu[xi]) +
+                 Md[xi] * (fabs(a) * e * fabs(h[n]) + fabs(bv * x)) + MA[d * N + n] * dt * e * fabs(h[n]);
+          h[n] = e * h[n] + dt * bv * x;
+          acc += fabs(Cm[bi + n]) * H[n] + MC[bi + n] * fabs(h[n]);
+        }
+        My[xi] = acc + fabs(Dv[d]) * Mu[xi] + MD[d] * fabs(x);
+      }
+    }
+  }
+  return 0;
+}
+
+int oracle_scan_mag_vjp(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                        const double* u, const double* delta, const double* A,
+                        const double* Bm, const double* Cm, const double* Dv,
+                        const double* Mu, const double* Md, const double* MA,
+                        const double* MB, const double* MC, const double* MD,
+                        const double* g, const double* Mg, double* Mdu,
+                        double* Mdd, double* MdA, double* MdB, double* MdC,
+                        double* MdD) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+  const int64_t nbl = Bsz * L * N;
+  memset(MdA, 0, sizeof(double) * (size_t)(D * N));
+  memset(MdB, 0, sizeof(double) * (size_t)nbl);
+  memset(MdC, 0, sizeof(double) * (size_t)nbl);
+  memset(MdD, 0, sizeof(double) * (size_t)D);
+  int fail = 0;
+#pragma omp parallel
+  {
+    /* hs / Hs[(t+1)*N + n] = h_t / H_t, [0..N) = 0 */
+    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    double* Hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    double* lB = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lC = (double*)calloc((size_t)nbl, sizeof(double));
+    double* lA = (double*)calloc((size_t)(D * N), sizeof(double));
+    double* lD = (double*)calloc((size_t)D, sizeof(double));
+    const int ok = hs && Hs && lB && lC && lA && lD;
+    if (!ok) {
+#pragma omp atomic write
+      fail = 1;
+    }
+#pragma omp for collapse(2) schedule(static)
+    for (int64_t b = 0; b < Bsz; ++b) {
+      for (int64_t d = 0; d < D; ++d) {
+        if (!ok) continue;
+        for (int64_t n = 0; n < N; ++n) hs[n] = Hs[n] = 0.0;
+        for (int64_t t = 0; t < L; ++t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi];
+          for (int64_t n = 0; n < N; ++n) {
+            const double a = A[d * N + n];
+            const double e = exp(dt * a);
+            const double bv = Bm[bi + n];
+            const double hp = fabs(hs[t * N + n]);
+            Hs[(t + 1) * N + n] = e * Hs[t * N + n] + dt * (MB[bi + n] * fabs(x) + fabs(bv) * Mu[xi]) +
+                                  Md[xi] * (fabs(a) * e * hp + fabs(bv * x)) + MA[d * N + n] * dt * e * hp;
+            hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * bv * x;
+          }
+        }
+        double lam[64], lM[64];
+        for (int64_t n = 0; n < N; ++n) lam[n] = lM[n] = 0.0;
+        double dDacc = 0.0;
+        for (int64_t t = L - 1; t >= 0; --t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi], gy = g[xi], mg = Mg[xi];
+          const double mu = Mu[xi], md = Md[xi];
+          dDacc += mg * fabs(x) + fabs(gy) * mu;
+          double su = 0.0, sd = 0.0;
+          for (int64_t n = 0; n < N; ++n) {
+            const double a = A[d * N + n];
+            const double ma = MA[d * N + n];
+            const double e = exp(dt * a);
+            const double me = e * (1.0 + fabs(a) * md + dt * ma);
+            const double bv = Bm[bi + n], mb = MB[bi + n];
+            const double hp = fabs(hs[t * N + n]), Hp = Hs[t * N + n];
+            /* lam, lM now hold the values carried in from t+1 (already
+             * multiplied by e_{t+1} / with Me_{t+1} |lam_{t+1}| added) */
+            lam[n] += Cm[bi + n] * gy;
+            lM[n] += fabs(Cm[bi + n]) * mg + MC[bi + n] * fabs(gy);
+            const double al = fabs(lam[n]);
+            su += dt * fabs(bv) * lM[n] + (md * fabs(bv) + dt * mb) * al;
+            sd += lM[n] * (fabs(a) * e * hp + fabs(bv * x)) +
+                  al * (ma * e * hp + fabs(a) * me * hp + fabs(a) * e * Hp + mb * fabs(x) + fabs(bv) * mu);
+            lA[d * N + n] += lM[n] * dt * e * hp + al * (md * e * hp + dt * me * hp + dt * e * Hp);
+            lB[bi + n] += lM[n] * dt * fabs(x) + al * (md * fabs(x) + dt * mu);
+            lC[bi + n] += mg * fabs(hs[(t + 1) * N + n]) + fabs(gy) * Hs[(t + 1) * N + n];
+            /* carry to t-1: lam_{t-1} gets e_t lam_t, lM_{t-1} gets e_t lM_t + Me_t |lam_t| */
+            lM[n] = e * lM[n] + me * al;
+            lam[n] *= e;
+          }
+          Mdu[xi] = fabs(Dv[d]) * mg + MD[d] * fabs(gy) + su;
+          Mdd[xi] = sd;
+        }
+        lD[d] += dDacc;
+      }
+    }
+#pragma omp critical
+    if (ok) {
+      for (int64_t i = 0; i < nbl; ++i) { MdB[i] += lB[i]; MdC[i] += lC[i]; }
+      for (int64_t i = 0; i < D * N; ++i) MdA[i] += lA[i];
+      for (int64_t i = 0; i < D; ++i) MdD[i] += lD[i];
+    }
+    free(hs); free(Hs); free(lB); free(lC); free(lA); free(lD);
+  }
+  return fail ? -2 : 0;
+}

@@ -278,3 +278,337 @@ def softplus_inverse(dt):
 def dt_rank_for(d_model):
     """mamba_block.py:136."""
     return math.ceil(d_model / 16)
+
+
+# ---------------------------------------------------------------------------
+# Error-magnitude companions (per-element bounds for the module parity tests)
+# ---------------------------------------------------------------------------
+#
+# A first-order running error analysis of the restatements above, carried
+# out alongside them.  Every tensor is a pair TC(v, m): its float64 value v
+# and an error magnitude m >= |v| in units of 2^-24 (a float32 evaluation is
+# expected within a small multiple of 2^-24 m of v).  Each operation with
+# coefficients is an autograd Function over both channels:
+#   forward   m_out = magnitudes of the terms forming the output with the
+#             errors of the inputs (one magnitude times values per term);
+#   backward  given the actual cotangent G and its magnitude MG, the value
+#             channel gets the true gradient and the magnitude channel the
+#             magnitude of that gradient's terms with the errors of their
+#             factors (the cotangent's and the forward values').
+# Shape-only operations (permute, flip, pad, slices, adds) act on both
+# channels.  So one backward of <G, out.v> + <|G|, out.m> gives, for every
+# parameter and input, the true gradient (value leaves) and its magnitude S
+# (magnitude leaves: |p|, ones for A_log).  The value channel reproduces
+# the restatements above (tests/test_oracle_blocks.py checks values and
+# gradients against torch autograd of them).
+
+class TC:
+    """A (value, magnitude) pair."""
+
+    def __init__(self, v, m):
+        self.v, self.m = v, m
+
+    def map(self, fn):
+        return TC(fn(self.v), fn(self.m))
+
+    def __add__(self, other):
+        return TC(self.v + other.v, self.m + other.m)
+
+    def __getitem__(self, idx):
+        return TC(self.v[idx], self.m[idx])
+
+    def flip(self, dim):
+        return TC(self.v.flip(dim), self.m.flip(dim))
+
+
+def _reduce_to(t, shape):
+    return t.sum_to_size(shape) if t.shape != shape else t
+
+
+class _LinFn(torch.autograd.Function):
+    """Y = X W^T."""
+
+    @staticmethod
+    def forward(ctx, X, MX, W, MW):
+        ctx.save_for_backward(X, MX, W, MW)
+        return X @ W.T, MX @ MW.T
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        X, MX, W, MW = ctx.saved_tensors
+        Xf, MXf = X.reshape(-1, X.shape[-1]), MX.reshape(-1, X.shape[-1])
+        Gf, MGf = G.reshape(-1, G.shape[-1]), MG.reshape(-1, G.shape[-1])
+        dW = Gf.T @ Xf
+        MdW = MGf.T @ Xf.abs() + Gf.abs().T @ MXf
+        return G @ W, MG @ MW, dW, MdW
+
+
+class _MulFn(torch.autograd.Function):
+    """a * b (broadcasting)."""
+
+    @staticmethod
+    def forward(ctx, a, Ma, b, Mb):
+        ctx.save_for_backward(a, Ma, b, Mb)
+        return a * b, Ma * b.abs() + a.abs() * Mb
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        a, Ma, b, Mb = ctx.saved_tensors
+        da, db = G * b, G * a
+        Mda = MG * b.abs() + G.abs() * Mb
+        Mdb = MG * a.abs() + G.abs() * Ma
+        return (_reduce_to(da, a.shape), _reduce_to(Mda, a.shape),
+                _reduce_to(db, b.shape), _reduce_to(Mdb, b.shape))
+
+
+def _pw_terms(kind, x):
+    """(f, f', magnitude of the terms of f', a bound on |f''|)."""
+    s = torch.sigmoid(x)
+    if kind == "silu":
+        return (x * s, s * (1 + x * (1 - s)), s * (1 + x.abs() * (1 - s)),
+                s * (1 - s) * (2 + x.abs() * (1 - 2 * s).abs()))
+    return F.softplus(x), s, s, s * (1 - s)   # softplus
+
+
+class _PointwiseFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, Mx, kind):
+        ctx.save_for_backward(x, Mx)
+        ctx.kind = kind
+        f, df, _, _ = _pw_terms(kind, x)
+        return f, f.abs() + df.abs() * Mx
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        x, Mx = ctx.saved_tensors
+        _, df, cdf, d2f = _pw_terms(ctx.kind, x)
+        return G * df, MG * cdf + G.abs() * d2f * Mx, None
+
+
+class _NegExpFn(torch.autograd.Function):
+    """A = -exp(A_log) (mamba_block.py:184); the magnitude leaf is ones."""
+
+    @staticmethod
+    def forward(ctx, a_log, ones):
+        A = -torch.exp(a_log)
+        ctx.save_for_backward(A)
+        return A, A.abs() * ones
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        (A,) = ctx.saved_tensors
+        return G * A, (MG + G.abs()) * A.abs()
+
+
+class _LayerNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, Mx, w, Mw, b, Mb, eps):
+        mu = x.mean(-1, keepdim=True)
+        var = ((x - mu) ** 2).mean(-1, keepdim=True)
+        r = 1.0 / torch.sqrt(var + eps)
+        xh = (x - mu) * r
+        E = r * (Mx + Mx.mean(-1, keepdim=True) + xh.abs() * (xh.abs() * Mx).mean(-1, keepdim=True)) + xh.abs()
+        # relative error of r (half that of var), in units of 2^-24
+        rho = 1 + 0.5 * ((2 * (x - mu).abs() * (Mx + Mx.mean(-1, keepdim=True))).mean(-1, keepdim=True)
+                         + var) / (var + eps)
+        ctx.save_for_backward(xh, r, E, rho, w, Mw)
+        return xh * w + b, E * w.abs() + Mw * xh.abs() + Mb
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        xh, r, E, rho, w, Mw = ctx.saved_tensors
+        g = G * w
+        Mg = MG * Mw
+        mg, mgx = g.mean(-1, keepdim=True), (g * xh).mean(-1, keepdim=True)
+        dx = r * (g - mg - xh * mgx)
+        Mdx = (r * (Mg + Mg.mean(-1, keepdim=True) + xh.abs() * (Mg * xh.abs()).mean(-1, keepdim=True))
+               + r * (E * mgx.abs() + xh.abs() * (g.abs() * E).mean(-1, keepdim=True)) + dx.abs() * rho)
+        lead = tuple(range(G.dim() - 1))
+        dw = (G * xh).sum(lead)
+        Mdw = (MG * xh.abs() + G.abs() * E).sum(lead)
+        return dx, Mdx, dw, Mdw, G.sum(lead), MG.sum(lead), None
+
+
+class _ScanFn(torch.autograd.Function):
+    """The scan (float64 C oracle) and its error magnitudes."""
+
+    @staticmethod
+    def forward(ctx, u, Mu, dl, Md, A, MA, B, MB, C, MC, D, MD):
+        vals = [t.detach().numpy() for t in (u, dl, A, B, C, D)]
+        mags = [t.detach().numpy() for t in (Mu, Md, MA, MB, MC, MD)]
+        ctx.vals, ctx.mags = vals, mags
+        return (torch.from_numpy(ref_lib.scan_fwd_f64(*vals)),
+                torch.from_numpy(ref_lib.scan_mag_fwd(vals, mags)))
+
+    @staticmethod
+    def backward(ctx, G, MG):
+        g = G.detach().double().numpy()
+        grads = ref_lib.scan_vjp_f64(*ctx.vals, g)
+        mags = ref_lib.scan_mag_vjp(ctx.vals, ctx.mags, g, MG.detach().double().numpy())
+        out = []
+        for a, m in zip(grads, mags):
+            out += [torch.from_numpy(a), torch.from_numpy(m)]
+        return tuple(out)
+
+
+def tc_lin(x, W):
+    return TC(*_LinFn.apply(x.v, x.m, W.v, W.m))
+
+
+def tc_mul(a, b):
+    return TC(*_MulFn.apply(a.v, a.m, b.v, b.m))
+
+
+def tc_pointwise(kind, x):
+    return TC(*_PointwiseFn.apply(x.v, x.m, kind))
+
+
+def tc_params(params):
+    """TC leaves for the module parameters: the value leaves are ``params``
+    themselves (their .grad is the true gradient), the magnitude leaves |p|
+    (ones for A_log; their .grad is the gradient's magnitude)."""
+    out = {}
+    for k, v in params.items():
+        m = torch.ones_like(v) if k.endswith("A_log") else v.detach().abs()
+        out[k] = TC(v, m.clone().requires_grad_(True))
+    return out
+
+
+def layer_norm_tc(P, prefix, x, eps=1e-5):
+    w, b = P[prefix + "weight"], P[prefix + "bias"]
+    return TC(*_LayerNormFn.apply(x.v, x.m, w.v, w.m, b.v, b.m, eps))
+
+
+def mamba_block_tc(P, prefix, x, d_state, d_conv):
+    """``mamba_block`` on TC pairs."""
+    Q = {k[len(prefix):]: v for k, v in P.items() if k.startswith(prefix)}
+    L = x.v.shape[1]
+    d_inner = Q["out_proj.weight"].v.shape[1]
+    dt_rank = Q["dt_proj.weight"].v.shape[1]
+    xz = tc_lin(x, Q["in_proj.weight"])
+    xb, z = xz[..., :d_inner], xz[..., d_inner:]
+    xp = xb.map(lambda t: F.pad(t, (0, 0, d_conv - 1, 0)))
+    cw = Q["conv1d.weight"]
+    pre = Q["conv1d.bias"]
+    for j in range(d_conv):
+        pre = pre + tc_mul(xp[:, j:j + L], cw[:, 0, j])
+    xc = tc_pointwise("silu", pre)
+    dbc = tc_lin(xc, Q["x_proj.weight"])
+    dt = dbc[..., :dt_rank]
+    Bm = dbc[..., dt_rank:dt_rank + d_state]
+    Cm = dbc[..., dt_rank + d_state:]
+    delta = tc_pointwise("softplus", tc_lin(dt, Q["dt_proj.weight"]) + Q["dt_proj.bias"])
+    A = TC(*_NegExpFn.apply(Q["A_log"].v, Q["A_log"].m))
+    Dp = Q["D"]
+    y = TC(*_ScanFn.apply(xc.v, xc.m, delta.v, delta.m, A.v, A.m, Bm.v, Bm.m, Cm.v, Cm.m,
+                          Dp.v, Dp.m))
+    y = tc_mul(y, tc_pointwise("silu", z))
+    return tc_lin(y, Q["out_proj.weight"])
+
+
+def residual_block_tc(P, prefix, x, d_state, d_conv):
+    """ResidualMambaBlock: x + mamba(norm(x)) (mamba_block.py:195-205)."""
+    return x + mamba_block_tc(P, prefix + "mamba.", layer_norm_tc(P, prefix + "norm.", x),
+                              d_state, d_conv)
+
+
+def bidirectional_block_tc(P, prefix, x, d_state, d_conv):
+    h = layer_norm_tc(P, prefix + "norm.", x)
+    yf = mamba_block_tc(P, prefix + "forward_mamba.", h, d_state, d_conv)
+    yb = mamba_block_tc(P, prefix + "backward_mamba.", h.flip(1), d_state, d_conv)
+    return x + yf + yb.flip(1)
+
+
+def direction_block_tc(P, prefix, x, num_directions, grid_shape, d_state, d_conv):
+    n = x.v.shape[1]
+    h = layer_norm_tc(P, prefix + "norm.", x)
+    expected = 1
+    for gdim in (grid_shape or (n,)):
+        expected *= gdim
+    K = num_directions
+    if n != expected and K > 2:
+        yf = mamba_block_tc(P, prefix + "mamba_blocks.0.", h, d_state, d_conv)
+        yb = mamba_block_tc(P, prefix + "mamba_blocks.1.", h.flip(1), d_state, d_conv)
+        return x + yf + yb.flip(1)
+    y = x
+    for k in range(K):
+        pair, rev = divmod(k, 2)
+        axes = _AXES[K][pair]
+        seq = h if axes is None else h.map(lambda t: _permute(t, grid_shape, axes))
+        if rev:
+            seq = seq.flip(1)
+        out = mamba_block_tc(P, f"{prefix}mamba_blocks.{k}.", seq, d_state, d_conv)
+        if rev:
+            out = out.flip(1)
+        if axes is not None:
+            out = out.map(lambda t: _unpermute(t, grid_shape, axes))
+        y = y + out
+    return y
+
+
+def vision_mamba_tc(P, x, *, input_dim, patch_size, depth, grid_shape, d_state, d_conv,
+                    temporal_patch_size=1, patch_indices=None):
+    """``vision_mamba`` on TC pairs (the patch embedding as a linear map of
+    the flattened patches)."""
+    if x.v.ndim != 3:
+        W = P["patch_embed.proj.weight"]
+        E = W.v.shape[0]
+        W2 = W.map(lambda t: t.reshape(E, -1))
+        p = patch_size
+        if input_dim == 2:
+            bsz, H, Wd, C = x.v.shape
+
+            def patches(t):
+                t = t.reshape(bsz, H // p, p, Wd // p, p, C).permute(0, 1, 3, 5, 2, 4)
+                return t.reshape(bsz, (H // p) * (Wd // p), C * p * p)
+        else:
+            if input_dim == 3:
+                bsz, Dd, H, Wd, C = x.v.shape
+                fold = lambda t: t                                        # noqa: E731
+            else:
+                bsz0, T, Dd, H, Wd, C0 = x.v.shape
+                tp = temporal_patch_size
+
+                def fold(t):
+                    if tp > 1:
+                        t = t.reshape(bsz0, T // tp, tp, Dd, H, Wd, C0).permute(0, 1, 3, 4, 5, 2, 6)
+                        t = t.reshape(bsz0, T // tp, Dd, H, Wd, tp * C0)
+                    return t.reshape(bsz0 * (T // tp), Dd, H, Wd, -1)
+                C = C0 * tp
+                bsz = bsz0 * (T // tp)
+
+            def patches(t):
+                t = fold(t).reshape(bsz, Dd // p, p, H // p, p, Wd // p, p, C)
+                t = t.permute(0, 1, 3, 5, 7, 2, 4, 6)
+                return t.reshape(bsz, -1, C * p * p * p)
+        x = tc_lin(x.map(patches), W2) + P["patch_embed.proj.bias"]
+        if input_dim == 4:
+            x = x.map(lambda t: t.reshape(bsz0, -1, E))
+    pos = P["pos_embed"]
+    if patch_indices is not None:
+        pos = pos[:, patch_indices, :]
+    x = x + pos
+    K = {2: 4, 3: 6, 4: 8}[input_dim]
+    for i in range(depth):
+        x = direction_block_tc(P, f"blocks.{i}.", x, K, grid_shape, d_state, d_conv)
+    return layer_norm_tc(P, "norm.", x)
+
+
+def run_tc(fn, params, x, G):
+    """Runs a ``*_tc`` restatement on float64 parameter leaves ``params``
+    and input x with output cotangent G.  Returns (output, grads, S): the
+    output value, {"input grad", "grad <param>"} true gradients, and the
+    magnitudes {"output", "input grad", "grad <param>"}."""
+    P = tc_params(params)
+    xv = x.detach().double().clone().requires_grad_(True)
+    xm = xv.detach().abs().requires_grad_(True)
+    out = fn(P, TC(xv, xm))
+    G = G.detach().double()
+    ((G * out.v).sum() + (G.abs() * out.m).sum()).backward()
+    grads = {"input grad": xv.grad}
+    S = {"output": out.m.detach(), "input grad": xm.grad}
+    for k, t in P.items():
+        if t.m.grad is not None:
+            grads[f"grad {k}"] = t.v.grad
+            S[f"grad {k}"] = t.m.grad
+    return out.v.detach(), grads, S

@@ -12,8 +12,10 @@
 * Layout and mode corner cases: B and C broadcast over the batch, no_grad
   forwards, malformed direction tables.
 * Module parity at a real layer width: one MultiDirectionalMambaBlock of
-  the VisionMamba-2D encoder (E=384, d_inner=768, K=4, 14x14 grid) and of
-  the 4D encoder (K=8, grid (8, 4, 4, 4)), against the float64 restatement.
+  the VisionMamba-2D encoder (E=384, d_inner=768, K=4, 14x14 grid), of the
+  3D encoder (K=6, 16^3 grid) and of the 4D encoder (K=8, grid
+  (8, 4, 4, 4)), against the float64 restatement, at the per-element
+  module bound (tests/module_bounds.py).
 """
 
 import numpy as np
@@ -23,7 +25,7 @@ import torch
 import mlx_vision_mamba_amd as mvm
 from mlx_vision_mamba_amd import synthetic
 from oracle import ref_lib, torch_ref
-from tests.test_gpu_modules import _compare, _run_both
+from tests.test_gpu_modules import _compare, _dir_mag, _mamba_mag, _run_both
 from tests.test_gpu_scan import NAMES, assert_close, ddelta_scale, oracle
 
 pytestmark = pytest.mark.gpu
@@ -88,7 +90,7 @@ def test_replaced_scan_fn_is_called_in_a_block(cuda):
     rec = _Recorder()
     blk._scan_fn = rec
     x = torch.randn(2, 40, 32)
-    _run_both(blk, x, lambda p, xx: torch_ref.mamba_block(p, "", xx, 16, 4), cuda)
+    _run_both(blk, x, lambda p, xx: torch_ref.mamba_block(p, "", xx, 16, 4), cuda, _mamba_mag)
     assert rec.shapes == [((2, 40, 64), (2, 40, 64), (64, 16), (2, 40, 16), (2, 40, 16), (64,))]
 
 
@@ -103,11 +105,13 @@ def test_replaced_scan_fn_in_direction_blocks(cuda):
         recs.append(_Recorder())
         b._scan_fn = recs[-1]
     x = torch.randn(2, 20, 32)
-    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4), cuda)
+    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4), cuda,
+              _dir_mag(K, grid))
     assert all(len(r.shapes) == 1 for r in recs)
     bi = mvm.BidirectionalMambaBlock(d_model=32)
     bi.backward_mamba._scan_fn = _Recorder()
-    _run_both(bi, x, lambda p, xx: torch_ref.bidirectional_block(p, "", xx, 16, 4), cuda)
+    _run_both(bi, x, lambda p, xx: torch_ref.bidirectional_block(p, "", xx, 16, 4), cuda,
+              lambda P, X: torch_ref.bidirectional_block_tc(P, "", X, 16, 4))
     assert len(bi.backward_mamba._scan_fn.shapes) == 1
 
 
@@ -175,4 +179,5 @@ def test_direction_block_at_layer_width(cuda, K, grid, bsz):
     blk = mvm.MultiDirectionalMambaBlock(d_model=384, num_directions=K, grid_shape=grid)
     x = torch.randn(bsz, L, 384)
     _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4,
-                                                              scan=torch_ref.scan_oracle_c), cuda)
+                                                              scan=torch_ref.scan_oracle_c), cuda,
+              _dir_mag(K, grid))

@@ -3,10 +3,14 @@ of the reference (oracle/torch_ref.py), on identical weights and inputs.
 
 The product modules run in float32 on the GPU (hipBLASLt GEMMs, the HIP
 scan, index-remapped directions); the oracle runs the reference's
-formulation in float64 on the CPU (materialised permutations, sequential
-Python-loop scan, torch autograd).  Module tolerance, per tensor:
-|got - ref| <= 1e-4 * max|ref| + 1e-4 * |ref| for the output and for the
-gradient of every parameter and of the input.
+formulation in float64 on the CPU (materialised permutations, the scan
+through the float64 oracle, torch autograd).  Tolerance per element for
+the output and for the gradient of every parameter and of the input
+(tests/module_bounds.py):
+|got - ref| <= 1e-5 + 1e-4 |ref| + min(8 * 2^-24 * S, 1e-4 * max|ref|),
+S the magnitude companion's sum of the magnitudes of the terms that form
+the element with the errors of its factors (the running error analysis
+oracle/torch_ref.py ``*_tc``).
 """
 
 import pytest
@@ -14,26 +18,18 @@ import torch
 
 import mlx_vision_mamba_amd as mvm
 from oracle import torch_ref
+from tests import module_bounds as mbd
 
 pytestmark = pytest.mark.gpu
 
 
-def _compare(name, got, ref):
-    got = got.detach().double().cpu()
-    ref = ref.detach().double()
-    assert got.shape == ref.shape, (name, got.shape, ref.shape)
-    assert torch.isfinite(got).all(), name
-    scale = float(ref.abs().max()) if ref.numel() else 0.0
-    err = (got - ref).abs()
-    bound = 1e-4 * scale + 1e-4 * ref.abs()
-    if (err > bound).any():
-        i = int(torch.argmax(err - bound))
-        raise AssertionError(f"{name}: max err {float(err.max()):.3e} (scale {scale:.3e}); "
-                             f"worst flat index {i}: got {float(got.flatten()[i])}, "
-                             f"ref {float(ref.flatten()[i])}")
+def _compare(name, got, ref, S=None, log=None):
+    mbd.check(name, got, ref, S, log=log)
 
 
-def _run_both(module, x, oracle_fn, device):
+def _run_both(module, x, oracle_fn, device, tc_fn=None):
+    """Module on the GPU against the float64 restatement ``oracle_fn`` (and
+    its running error analysis ``tc_fn``, for the per-element bounds)."""
     torch.manual_seed(123)
     module = module.to(device)
     xg = x.to(device).requires_grad_(True)
@@ -44,17 +40,33 @@ def _run_both(module, x, oracle_fn, device):
     xr = x.double().clone().requires_grad_(True)
     yr = oracle_fn(params, xr)
     yr.backward(gy.double())
-    _compare("output", y, yr)
-    _compare("input grad", xg.grad, xr.grad)
-    _compare_grads(module, params)
+    S = {}
+    if tc_fn is not None:
+        _, S = mbd.magnitudes(tc_fn, params, x.double(), gy.double())
+    log = []
+    _compare("output", y, yr, S.get("output"), log)
+    _compare("input grad", xg.grad, xr.grad, S.get("input grad"), log)
+    _compare_grads(module, params, S, log)
+    if log:
+        name, worst = max(log, key=lambda t: t[1])
+        print(f"worst err / (2^-24 S) = {worst:.3f} ({name})", flush=True)
 
 
-def _compare_grads(module, params):
+def _compare_grads(module, params, S=None, log=None):
+    S = S or {}
     for n, p in module.named_parameters():
         if p.grad is None:   # not on the graph (e.g. patch_embed for token inputs)
             assert params[n].grad is None or not params[n].grad.any(), n
             continue
-        _compare(f"grad {n}", p.grad, params[n].grad)
+        _compare(f"grad {n}", p.grad, params[n].grad, S.get(f"grad {n}"), log)
+
+
+def _mamba_mag(P, X):
+    return torch_ref.mamba_block_tc(P, "", X, 16, 4)
+
+
+def _dir_mag(K, grid, d_state=16):
+    return lambda P, X: torch_ref.direction_block_tc(P, "", X, K, grid, d_state, 4)
 
 
 @pytest.mark.parametrize("mode", ["sequential", "chunked", "hip", "metal_fused", "parallel",
@@ -63,7 +75,7 @@ def test_mamba_block(cuda, mode):
     torch.manual_seed(0)
     blk = mvm.MambaBlock(d_model=32, d_state=16, scan_mode=mode)
     x = torch.randn(2, 40, 32)
-    _run_both(blk, x, lambda p, xx: torch_ref.mamba_block(p, "", xx, 16, 4), cuda)
+    _run_both(blk, x, lambda p, xx: torch_ref.mamba_block(p, "", xx, 16, 4), cuda, _mamba_mag)
 
 
 def test_residual_and_bidirectional(cuda):
@@ -73,9 +85,11 @@ def test_residual_and_bidirectional(cuda):
 
     def ref(p, xx):
         return xx + torch_ref.mamba_block(p, "mamba.", torch_ref.layer_norm(p, "norm.", xx), 16, 4)
-    _run_both(blk, x, ref, cuda)
+    _run_both(blk, x, ref, cuda,
+              lambda P, X: torch_ref.residual_block_tc(P, "", X, 16, 4))
     bi = mvm.BidirectionalMambaBlock(d_model=32)
-    _run_both(bi, x, lambda p, xx: torch_ref.bidirectional_block(p, "", xx, 16, 4), cuda)
+    _run_both(bi, x, lambda p, xx: torch_ref.bidirectional_block(p, "", xx, 16, 4), cuda,
+              lambda P, X: torch_ref.bidirectional_block_tc(P, "", X, 16, 4))
 
 
 @pytest.mark.parametrize("K,grid,n", [(2, None, 13), (4, (4, 5), 20), (6, (2, 3, 2), 12),
@@ -86,7 +100,8 @@ def test_multidirectional_block(cuda, K, grid, n):
     torch.manual_seed(2)
     blk = mvm.MultiDirectionalMambaBlock(d_model=32, num_directions=K, grid_shape=grid)
     x = torch.randn(2, n, 32)
-    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4), cuda)
+    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, K, grid, 16, 4), cuda,
+              _dir_mag(K, grid))
 
 
 @pytest.mark.parametrize("input_dim,shape,kw", [
@@ -100,11 +115,10 @@ def test_vision_mamba(cuda, input_dim, shape, kw):
                             input_dim=input_dim, **kw)
     x = torch.randn(*shape)
 
-    def ref(p, xx):
-        return torch_ref.vision_mamba(p, xx, input_dim=input_dim, patch_size=8, depth=2,
-                                      grid_shape=model.grid_shape, d_state=16, d_conv=4,
-                                      temporal_patch_size=kw.get("temporal_patch_size", 1))
-    _run_both(model, x, ref, cuda)
+    common = dict(input_dim=input_dim, patch_size=8, depth=2, grid_shape=model.grid_shape,
+                  d_state=16, d_conv=4, temporal_patch_size=kw.get("temporal_patch_size", 1))
+    _run_both(model, x, lambda p, xx: torch_ref.vision_mamba(p, xx, **common), cuda,
+              lambda P, X: torch_ref.vision_mamba_tc(P, X, **common))
 
 
 def test_vision_mamba_patch_subset(cuda):
@@ -137,8 +151,13 @@ def test_vision_mamba_patch_subset(cuda):
     xr = x.double().clone().requires_grad_(True)
     yr = ref(params, xr)
     yr.backward(gy.double())
-    _compare("output", y, yr)
-    _compare_grads(model, params)
+    _, S = mbd.magnitudes(
+        lambda P, X: torch_ref.vision_mamba_tc(
+            P, X, input_dim=2, patch_size=8, depth=2, grid_shape=model.grid_shape,
+            d_state=16, d_conv=4, patch_indices=idx), params, x.double(), gy.double())
+    _compare("output", y, yr, S["output"])
+    _compare("input grad", xg.grad, xr.grad, S["input grad"])
+    _compare_grads(model, params, S)
 
 
 def test_direction_block_small_state_ragged_channels(cuda):
@@ -148,7 +167,8 @@ def test_direction_block_small_state_ragged_channels(cuda):
     blk = mvm.MultiDirectionalMambaBlock(d_model=24, d_state=8, num_directions=4,
                                          grid_shape=(3, 4))
     x = torch.randn(3, 12, 24)
-    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, 4, (3, 4), 8, 4), cuda)
+    _run_both(blk, x, lambda p, xx: torch_ref.direction_block(p, "", xx, 4, (3, 4), 8, 4), cuda,
+              _dir_mag(4, (3, 4), 8))
 
 
 def _train_steps(model, x, steps):
@@ -246,7 +266,8 @@ def test_metal_mode_is_forward_only(cuda):
     params = torch_ref.params_from_module(blk)
     with torch.no_grad():
         yr = torch_ref.mamba_block(params, "", x.double(), 16, 4)
-    _compare("output", y, yr)
+    _, S = mbd.magnitudes(_mamba_mag, params, x.double(), torch.ones(yr.shape, dtype=torch.float64))
+    _compare("output", y, yr, S["output"])
     y.sum().backward()
     assert blk.out_proj.weight.grad is not None
     for name in ("in_proj", "x_proj", "dt_proj", "conv1d"):

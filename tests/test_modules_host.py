@@ -149,6 +149,21 @@ def test_permutation_check_on_host_tables():
     scan.check_permutation_table(torch.zeros(3, 0, dtype=torch.int32))
 
 
+def test_host_table_is_checked_on_the_callers_tensor():
+    """selective_scan_directions checks a host-memory table before copying
+    it to the device, so the check's stamp sticks to the tensor the caller
+    keeps and is not repeated for every fresh device copy (the call itself
+    then stops at the CPU tensors: there is no CPU fallback)."""
+    from mlx_vision_mamba_amd import scan
+    K, L, D, N = 2, 6, 8, 4
+    t = dirs.seq_to_tok_table(K, L, None)
+    u = torch.randn(1, L, K, D)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        scan.selective_scan_directions(u, u.abs(), -torch.ones(K, D, N), torch.randn(1, L, K, N),
+                                       torch.randn(1, L, K, N), torch.ones(K, D), seq_to_tok=t)
+    assert t._mvm_perm_checked == (t.data_ptr(), t._version)
+
+
 def test_replaced_scan_fn_is_detected():
     blk = mb.MambaBlock(16, scan_mode="chunked")
     assert not mb._custom_scan(blk)

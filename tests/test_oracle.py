@@ -367,3 +367,92 @@ def test_fp32_reference_algorithm_needs_the_ddelta_cancellation_term():
         assert plain.sum() >= 1            # the plain bar is out of reach in float32
         ratio = err / (2.0 ** -24 * S)
         assert ratio.max() <= 32.0, ratio.max()
+
+
+# ------------------------------------------------ scan magnitude companion
+
+def _mag_inputs(seed, bsz=2, L=30, D=5, N=8, a_zero=False):
+    rng = np.random.default_rng(seed)
+    u = rng.standard_normal((bsz, L, D))
+    dl = rng.uniform(0.01, 0.3, (bsz, L, D))
+    A = np.zeros((D, N)) if a_zero else -rng.uniform(0.5, 4.0, (D, N))
+    Bm, Cm = rng.standard_normal((bsz, L, N)), rng.standard_normal((bsz, L, N))
+    Dv = rng.standard_normal(D)
+    return u, dl, A, Bm, Cm, Dv
+
+
+def _zero_mags(vals):
+    return [np.zeros_like(v) for v in vals]
+
+
+def test_scan_magnitude_reduces_to_plain_scans():
+    """With the input magnitudes set to the inputs' absolute values the
+    companion is a scan of absolute values (oracle_scan_fwd); with unit
+    decay (A = 0) the delta magnitude enters as an added delta."""
+    vals = _mag_inputs(50)
+    u, dl, A, Bm, Cm, Dv = vals
+    absu, absB, absC = np.abs(u), np.abs(Bm), np.abs(Cm)
+    m = _zero_mags(vals)
+    m[0], m[3] = absu, absB
+    base = ref_lib.scan_fwd_f64(absu, dl, A, absB, absC, np.zeros_like(Dv))
+    np.testing.assert_allclose(ref_lib.scan_mag_fwd(vals, m), 2 * base + np.abs(Dv) * absu, rtol=1e-12)
+    m[4], m[5] = absC, np.abs(Dv)
+    _, hs = so.scan_fwd(*vals, return_states=True)          # the signed states h
+    ch = np.einsum("bldn,bln->bld", np.abs(hs), absC)
+    np.testing.assert_allclose(ref_lib.scan_mag_fwd(vals, m), 2 * base + ch + 2 * np.abs(Dv) * absu,
+                               rtol=1e-12)
+    vals0 = _mag_inputs(51, a_zero=True)
+    m0 = _zero_mags(vals0)
+    m0[0], m0[3] = np.abs(vals0[0]), np.abs(vals0[3])
+    m0[1] = np.random.default_rng(52).uniform(0.0, 0.2, vals0[1].shape)
+    expect = ref_lib.scan_fwd_f64(np.abs(vals0[0]), 2 * vals0[1] + m0[1], vals0[2],
+                                  np.abs(vals0[3]), np.abs(vals0[4]), np.zeros(vals0[0].shape[2]))
+    expect += np.abs(vals0[5]) * np.abs(vals0[0])
+    np.testing.assert_allclose(ref_lib.scan_mag_fwd(vals0, m0), expect, rtol=1e-12)
+
+
+@pytest.mark.parametrize("which", [1, 2])
+def test_scan_magnitude_bounds_finite_differences(which):
+    """A perturbation of delta (which=1) or A (which=2) by eta * M moves y by
+    at most eta times the part of My that M adds (first order; M(u) = |u|
+    and M(B) = |B| as the companion requires): the companion bounds the
+    scan's sensitivity to the errors of its inputs, signs and cancellation
+    included."""
+    vals = _mag_inputs(53 + which)
+    rng = np.random.default_rng(60 + which)
+    m = _zero_mags(vals)
+    m[0], m[3] = np.abs(vals[0]), np.abs(vals[3])   # the companion's premise: M(u), M(B) >= |.|
+    base = ref_lib.scan_mag_fwd(vals, m)
+    m[which] = rng.uniform(0.0, 1.0, vals[which].shape) * np.abs(vals[which])
+    My = ref_lib.scan_mag_fwd(vals, m) - base
+    eta = 1e-6
+    pert = list(vals)
+    pert[which] = vals[which] + eta * m[which]
+    dy = np.abs(ref_lib.scan_fwd_f64(*pert) - ref_lib.scan_fwd_f64(*vals)) / eta
+    assert np.all(dy <= My * (1 + 1e-4) + 1e-9)
+    assert np.max(dy / np.maximum(My, 1e-300)) > 0.05      # not vacuous
+
+
+def test_scan_error_magnitudes_bound_the_float32_scan():
+    """The error magnitudes of y and of the six gradients (scan_ref.c
+    oracle_scan_mag_fwd / _vjp, exact inputs: M = |input|, Mg = |g|) are at
+    least the absolute values they stand for, and the reference's own
+    sequential algorithm run in float32 (torch_ref.scan_sequential with
+    autograd) is within 2 * 2^-24 * M of the float64 oracle, element by
+    element."""
+    inputs = scan_inputs.make(2, 60, 24, 16, seed=58, a_mode="random")
+    vals = [t.double().numpy() for t in inputs[:6]]
+    g = inputs[6].double().numpy()
+    mags = [np.abs(v) for v in vals]
+    My = ref_lib.scan_mag_fwd(vals, mags)
+    Mg = ref_lib.scan_mag_vjp(vals, mags, g, np.abs(g))
+    y = ref_lib.scan_fwd_f64(*vals)
+    grads = ref_lib.scan_vjp_f64(*vals, g)
+    leaves = [t.clone().requires_grad_(True) for t in inputs[:6]]
+    y32 = torch_ref.scan_sequential(*leaves)
+    got = [y32] + list(torch.autograd.grad(y32, leaves, inputs[6]))
+    for name, a, r, M in zip(["y", "du", "ddelta", "dA", "dB", "dC", "dD"], got, [y, *grads],
+                             [My, *Mg]):
+        assert np.all(M >= np.abs(r) * (1 - 1e-12)), name
+        err = np.abs(a.detach().double().numpy() - r)
+        assert np.all(err <= 2 * 2.0 ** -24 * M), (name, float(np.max(err / (2.0 ** -24 * M))))

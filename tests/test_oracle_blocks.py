@@ -325,3 +325,81 @@ def test_c_oracle_scan_op_equals_the_sequential_restatement(K, grid):
     with pytest.raises(ValueError):
         torch_ref.scan_oracle_c(*[torch.zeros(1, 2, 3)] * 2, torch.zeros(3, 4),
                                 *[torch.zeros(1, 2, 4)] * 2, torch.zeros(3))
+
+
+# ------------------------------------------------- magnitude companions
+
+from tests import module_bounds as mbd  # noqa: E402
+
+
+def _mag_case(kind):
+    """(module, input shape, restatement, TC restatement) for each kind."""
+    if kind == "mamba":
+        blk = mb.MambaBlock(d_model=16, d_state=16)
+        return blk, (2, 9, 16), (lambda p, x: torch_ref.mamba_block(p, "", x, 16, 4)), \
+            (lambda P, X: torch_ref.mamba_block_tc(P, "", X, 16, 4))
+    if kind == "residual":
+        blk = mb.ResidualMambaBlock(d_model=16)
+        return blk, (2, 9, 16), (lambda p, x: x + torch_ref.mamba_block(
+            p, "mamba.", torch_ref.layer_norm(p, "norm.", x), 16, 4)), \
+            (lambda P, X: torch_ref.residual_block_tc(P, "", X, 16, 4))
+    if kind == "bidirectional":
+        blk = mb.BidirectionalMambaBlock(d_model=16)
+        return blk, (2, 9, 16), (lambda p, x: torch_ref.bidirectional_block(p, "", x, 16, 4)), \
+            (lambda P, X: torch_ref.bidirectional_block_tc(P, "", X, 16, 4))
+    if kind.startswith("dir"):
+        K, grid, n = {"dir2": (2, None, 7), "dir4": (4, (3, 4), 12), "dir6": (6, (2, 3, 2), 12),
+                      "dir8": (8, (2, 1, 2, 3), 12), "dir4fallback": (4, (3, 4), 5)}[kind]
+        blk = mb.MultiDirectionalMambaBlock(d_model=16, num_directions=K, grid_shape=grid)
+        return blk, (2, n, 16), (lambda p, x: torch_ref.direction_block(p, "", x, K, grid, 16, 4)), \
+            (lambda P, X: torch_ref.direction_block_tc(P, "", X, K, grid, 16, 4))
+    dim = int(kind[-2])
+    kw = {2: {}, 3: {}, 4: {"num_temporal_frames": 4, "temporal_patch_size": 2}}[dim]
+    shape = {2: (2, 16, 16, 1), 3: (1, 8, 8, 8, 1), 4: (1, 4, 8, 8, 8, 1)}[dim]
+    model = vm.VisionMamba(img_size=shape[-2], patch_size=4, embed_dim=16, depth=2, input_dim=dim,
+                           **kw)
+    common = dict(input_dim=dim, patch_size=4, depth=2, grid_shape=model.grid_shape, d_state=16,
+                  d_conv=4, temporal_patch_size=kw.get("temporal_patch_size", 1))
+    return model, shape, (lambda p, x: torch_ref.vision_mamba(p, x, **common)), \
+        (lambda P, X: torch_ref.vision_mamba_tc(P, X, **common))
+
+
+MAG_KINDS = ["mamba", "residual", "bidirectional", "dir2", "dir4", "dir6", "dir8", "dir4fallback",
+             "vm2d", "vm3d", "vm4d"]
+
+
+@pytest.mark.parametrize("kind", MAG_KINDS)
+def test_error_magnitudes_bound_the_restatements(kind):
+    """The ``*_tc`` running error analysis: its value channel reproduces the
+    restatement's output and every gradient (its backward formulas are
+    checked against torch autograd of the restatement); every magnitude is
+    at least the absolute value it stands for; and the restatement
+    evaluated in float32 (the reference's precision) is within
+    2 * 2^-24 * S of the float64 values, element by element (the module
+    parity tests allow 8 * 2^-24 * S, module_bounds.C_MOD)."""
+    torch.manual_seed(70)
+    module, shape, ref_fn, tc_fn = _mag_case(kind)
+    x = torch.randn(*shape, dtype=torch.float64)
+    p = torch_ref.params_from_module(module)
+    xr = x.clone().requires_grad_(True)
+    y = ref_fn(p, xr)
+    G = torch.randn(y.shape, dtype=torch.float64)
+    y.backward(G)
+    val, grads, S = torch_ref.run_tc(tc_fn, torch_ref.params_from_module(module), x, G)
+    np.testing.assert_allclose(_np(val), _np(y), rtol=1e-12, atol=1e-13)
+    refs = {"output": y.detach(), "input grad": xr.grad}
+    refs.update({f"grad {k}": v.grad for k, v in p.items() if v.grad is not None})
+    assert set(refs) == set(S)
+    for name, r in refs.items():
+        if name != "output":
+            np.testing.assert_allclose(_np(grads[name]), _np(r), rtol=1e-10, atol=1e-12, err_msg=name)
+        assert bool((S[name] >= r.abs() * (1 - 1e-12)).all()), name
+    # float32 evaluation of the same restatement
+    p32 = {k: v.detach().float().requires_grad_(True) for k, v in p.items()}
+    x32 = x.float().requires_grad_(True)
+    y32 = ref_fn(p32, x32)
+    y32.backward(G.float())
+    got = {"output": y32.detach(), "input grad": x32.grad}
+    got.update({f"grad {k}": v.grad for k, v in p32.items() if v.grad is not None})
+    for name, r in refs.items():
+        mbd.check(name, got[name], r, S[name], c=2, cap=False)
