@@ -525,17 +525,17 @@ def cpu_baseline(torch):
 
     step()  # warm-up
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-    dt = sorted(times)[1]
+    dt = sorted(times)[2]
     scan_cpu = cpu_scan_baseline(torch)
     return {"value": round(2 / dt, 3), "unit": "imgs/s", "cores": cores, "kind": "port",
             "cpu_model": cpu_model(),
             "sample": "VisionMamba-2D K=4 step (fwd + mean loss + bwd), batch 2 of the same "
                       "224x224x1 / patch 16 / E=384 / depth 6 model, float32, reference's "
-                      "sequential scan restated in torch; 1 warm-up, median of 3 timed steps",
+                      "sequential scan restated in torch; 1 warm-up, median of 5 timed steps",
             "seconds_per_step": round(dt, 2), "step_seconds": [round(t, 2) for t in times],
             "scan": scan_cpu}
 
@@ -678,6 +678,10 @@ def main():
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": measured_traffic("bwd_call_hbm_bytes"),
+        # traffic and valu_busy_per_simd are not measured by this run: they
+        # are read from the committed rocprofv3 counter summary named here
+        "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) + " (rocprofv3 FETCH_SIZE / "
+                          "WRITE_SIZE, committed summary; not measured by this run)",
         "kernel": BWD_KERNELS,
         "algorithmic_bytes_per_launch": int(bwd_b), "avg_launch_us": round(bwd_t * 1e6, 2),
         "launches": len(bwd),
@@ -686,6 +690,8 @@ def main():
         # the backward is VALU-issue bound: share of the kernel's time the
         # SIMDs' VALU is issuing (VALUBusy counter, committed profile)
         "valu_busy_per_simd": measured_traffic("bwd_valu_busy_per_simd", float),
+        "valu_busy_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) + " (rocprofv3 VALUBusy, "
+                            "committed summary; not measured by this run)",
         # secondary: the reference formula's flop rate over the fused fwd +
         # VJP calls (B*K = 128 scans of L = 196, D = 768, N = 16)
         "secondary_flops": secondary_flops(32 * 4 * 196 * 768 * 16, fwd_t + bwd_t),
@@ -700,6 +706,9 @@ def main():
     # the SIMDs' VALU is issuing (VALUBusy counter, committed profile)
     scans["long_B8_L16384_bf16"]["valu_busy_per_pass"] = {
         p: measured_traffic("long_valu_busy_" + p, float, LONG_PROFILE) for p in LONG_PASSES}
+    scans["long_B8_L16384_bf16"]["valu_busy_source"] = (
+        os.path.relpath(LONG_PROFILE, ROOT) + " (rocprofv3 VALUBusy, committed summary; not "
+        "measured by this run)")
     out = {
         "metric": METRIC, "value": round(imgs, 2), "unit": "imgs/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,

@@ -35,8 +35,9 @@
 //
 // Fused form (FUSE, float32): delta = softplus(delta_raw + dt_bias) is
 // applied as the delta tile is staged; the stored gradient is that of
-// delta_raw, ddelta * sigmoid(delta_raw + dt_bias), with sigmoid recovered
-// from the staged delta as 1 - exp(-delta); dt_bias's gradient is its sum
+// delta_raw, ddelta * sigmoid(delta_raw + dt_bias), the sigmoid formed from
+// the softplus' own exponential when the tile is staged and kept in LDS
+// until the tile is flushed; dt_bias's gradient is its sum
 // over (b, t), reduced like dD.  The gate y = y_raw * silu(z) is undone as
 // the upstream gradient is staged: the scan consumes g = dy * silu(z), and
 // dz = dy * y_raw * silu'(z) is written from the same registers, so the
@@ -227,6 +228,9 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   __shared__ float sRed[kLean ? 1 : 2][4][kSub][2][kStatePad];
   __shared__ double sAcc[5][kLean ? kThreads : 1];
   __shared__ double sDb[4][kChPerBlock];  // fused: per-wave dt_bias gradient sums
+  // fused: sigmoid(delta_raw + dt_bias) of the staged tile, the softplus
+  // derivative applied to ddelta when the tile is flushed
+  __shared__ float sSg[FUSE ? 2 : 1][FUSE ? kSub : 1][kChPerBlock];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -351,10 +355,13 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // gradient summed over the rows this thread flushes
   const float dbias_l = (FUSE && bf.dbias != nullptr && cok) ? bf.dbias[k * gm.D + dld] : 0.f;
   double dbacc = 0.0;
+  // softplus of the staged delta_raw + dt bias, with its sigmoid (the
+  // softplus derivative) from the same exponential
+  float psg[4];
   auto stage_delta = [&](float (&v)[4]) {
     if (FUSE) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = softplus_f(v[r] + dbias_l);
+      for (int r = 0; r < 4; ++r) softplus_sigmoid(v[r] + dbias_l, v[r], psg[r]);
     }
   };
   // fused gate: the upstream dy is the gradient of y_raw * silu(z); the scan
@@ -395,7 +402,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
         const float duv = sU[buf][tt][lane];
         float dd = sG[buf][tt][lane];
         if (FUSE) {
-          dd *= softplus_grad_from_value(sD[buf][tt][lane]);
+          dd *= sSg[buf][tt][lane];
           dbt += cok ? dd : 0.f;
         }
         if (cok) {
@@ -523,6 +530,7 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
     store_xtile(sU[buf], pu, tid);
     store_xtile(sD[buf], pd, tid);
     store_xtile(sG[buf], pg, tid);
+    if (FUSE) store_xtile(sSg[buf], psg, tid);
     sB[buf][stile_row(tid)][tid & 15] = pb;
     sC[buf][stile_row(tid)][tid & 15] = pc;
   };

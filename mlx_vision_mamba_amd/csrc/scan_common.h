@@ -72,34 +72,32 @@ __device__ __forceinline__ int64_t token_row(const int32_t* tok, int64_t t, int6
 // v_log_f32, v_rcp_f32: a few ulp) rather than the libm routines, which
 // cost ~10x the instructions in VALU-bound kernels.
 //
-// log(1 + y) for y in (0, 1]: a 5-term series below 1/64 (truncation
-// < y^6 / 6 relative), else ln2 * log2(1 + y) (the rounding of 1 + y is
-// < 2^-24 absolute, < 2e-6 relative there).
-// Both branches are evaluated and selected (no divergent control flow).
-__device__ __forceinline__ float log1p_unit(float y) {
-  const float series = y * fmaf(y, fmaf(y, fmaf(y, fmaf(y, 0.2f, -0.25f), 1.f / 3.f), -0.5f), 1.f);
-  const float direct = kLn2 * __builtin_amdgcn_logf(1.f + y);
-  return y < 0.015625f ? series : direct;
-}
-// softplus with torch.nn.functional's threshold (x > 20 -> x):
-// max(x, 0) + log(1 + e^-|x|)
+// softplus: max(x, 0) + log(1 + y), y = e^-|x| in (0, 1].
+// log(1 + y) = ln2 * log2(u) + (y - (u - 1)) with u = fl(1 + y): the second
+// term is the rounding error of u (exact), so the sum keeps y's relative
+// precision for small y (to first order in that rounding), and v_log_f32 is
+// within 2 ulp of log2 near 1 (measured on MI355X); softplus within 30 ulp
+// over x in [-30, 20], the error of e^-|x| from the rounded product
+// |x| log2(e) included.  torch's threshold (x > 20 -> x) needs no branch of
+// its own: there log(1 + y) < 2.1e-9 is below half an ulp of x, so the sum
+// rounds to x (and +inf stays +inf, NaN stays NaN).
+// The sigmoid of the same x comes from the same exponential:
+// sigmoid(x) = (x >= 0 ? 1 : y) / (1 + y).
 __device__ __forceinline__ float softplus_f(float x) {
   const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
-  const float r = fmaxf(x, 0.f) + log1p_unit(y);
-  return x > 20.f ? x : r;
+  const float u = 1.f + y;
+  return fmaxf(x, 0.f) + fmaf(kLn2, __builtin_amdgcn_logf(u), y - (u - 1.f));
+}
+__device__ __forceinline__ void softplus_sigmoid(float x, float& sp, float& sg) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  const float u = 1.f + y;
+  sp = fmaxf(x, 0.f) + fmaf(kLn2, __builtin_amdgcn_logf(u), y - (u - 1.f));
+  sg = (x >= 0.f ? 1.f : y) * __builtin_amdgcn_rcpf(u);
 }
 // 1 / (1 + e^-x); saturates to 0 / 1 without NaN for large |x|
 __device__ __forceinline__ float sigmoid_f(float x) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
-// d softplus(x) / dx = sigmoid(x) = 1 - e^-sp from the softplus value sp >= 0
-// (series below 1/64, where 1 - e^-sp would cancel)
-__device__ __forceinline__ float softplus_grad_from_value(float sp) {
-  const float series = sp * fmaf(sp, fmaf(sp, fmaf(sp, -1.f / 24.f, 1.f / 6.f), -0.5f), 1.f);
-  const float direct = 1.f - __builtin_amdgcn_exp2f(-sp * kLog2e);
-  return sp < 0.015625f ? series : direct;
-}
-
 // A of one (direction, channel, state): the array holds A itself, or A_log
 // with A = -exp(A_log) (mamba_block.py:184) when a_log is set.  Read once
 // per (d, n) by each block, so the accurate expf costs nothing measurable.
