@@ -8,6 +8,14 @@ incremented by a device op before the kernel, so the whole step can be
 captured in a HIP graph and replayed.  The first and second moments of all
 tensors are two flat float32 buffers.
 
+One difference from torch.optim.AdamW: there is a single step count for all
+tensors, advanced by every ``step()``, where torch keeps one per parameter
+and advances it only when that parameter has a gradient.  The two agree
+when every parameter has a gradient on every step (the VisionMamba train
+step); a parameter whose gradient is missing on some steps gets torch's
+moments but a bias correction computed from the global count.  The count
+is float32, exact up to 2^24 steps.
+
 The tensor table (parameter and gradient pointers) is rebuilt on the host
 only when a pointer changes: gradients set to None and re-created by the
 next backward change it every eager step; a captured step sees the graph's
