@@ -34,6 +34,8 @@ def _load():
         lib.oracle_scan_vjp.restype = ctypes.c_int
         lib.oracle_ddelta_scale.argtypes = [i64] * 4 + [fp] * 6 + [dp]
         lib.oracle_ddelta_scale.restype = ctypes.c_int
+        lib.oracle_dA_scale.argtypes = [i64] * 4 + [fp] * 6 + [dp]
+        lib.oracle_dA_scale.restype = ctypes.c_int
         lib.oracle_scan_fwd_f64.argtypes = [i64] * 4 + [dp] * 7
         lib.oracle_scan_fwd_f64.restype = ctypes.c_int
         lib.oracle_scan_vjp_f64.argtypes = [i64] * 4 + [dp] * 13
@@ -110,6 +112,22 @@ def ddelta_scale(u, delta, A, B, C, g):
                                  _p(C, fp), _p(g, fp), _p(out, ctypes.c_double))
     if rc != 0:
         raise RuntimeError(f"oracle_ddelta_scale failed ({rc})")
+    return out
+
+
+def dA_scale(u, delta, A, B, C, g):
+    """float64 S[d,n] = sum_{b,t} |lam_t delta_t e_t h_{t-1}|: the
+    cancellation scale of dA (see scan_ref.c)."""
+    lib = _load()
+    u, delta, A, B, C, g = map(_f32, (u, delta, A, B, C, g))
+    bsz, L, d = u.shape
+    n = A.shape[1]
+    out = np.empty((d, n), dtype=np.float64)
+    fp = ctypes.c_float
+    rc = lib.oracle_dA_scale(bsz, L, d, n, _p(u, fp), _p(delta, fp), _p(A, fp), _p(B, fp),
+                             _p(C, fp), _p(g, fp), _p(out, ctypes.c_double))
+    if rc != 0:
+        raise RuntimeError(f"oracle_dA_scale failed ({rc})")
     return out
 
 

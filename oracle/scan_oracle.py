@@ -33,6 +33,10 @@ The other oracle pieces are pinned in the same way:
   the ddelta bound): S >= |ddelta| everywhere, S = |ddelta| exactly on
   inputs whose terms share one sign (both terms exercised), the delta = 0
   closed form over a reverse cumsum, and homogeneity in g and u.
+* scan_ref.c ``oracle_dA_scale`` (the cancellation scale of dA, the sum of
+  the magnitudes of its lam delta e h terms): S >= |dA| everywhere,
+  S = dA exactly when every term is positive, a scalar brute-force loop on a
+  tiny case, S = 0 at L = 1, and homogeneity in g and u.
 * torch_ref ``scan_sequential`` / ``scan_chunked``: autograd and
   ``gradcheck`` (tests/test_oracle.py); ``mamba_block``, ``layer_norm``,
   ``direction_block``, ``bidirectional_block``, ``vision_mamba``: closed

@@ -211,6 +211,67 @@ int oracle_ddelta_scale(int64_t Bsz, int64_t L, int64_t D, int64_t N,
   return fail ? -2 : 0;
 }
 
+/* Cancellation scale of dA: S[d,n] = sum_{b,t} |lam_t delta_t e_t h_{t-1}|,
+ * the sum of the absolute values of the terms whose signed sum is dA[d,n]
+ * (mamba_metal_fused.py:122, :218; same recurrences as oracle_scan_vjp).
+ * dA sums B * L such terms, and with slow decays (|A| delta << 1) both
+ * lam and h grow over long stretches of the sequence, so an fp32
+ * evaluation of dA cannot be closer than some multiple of 2^-24 * S.
+ * Pinned in tests/test_oracle.py: S >= |dA|; S == |dA| when every term has
+ * one sign; S = 0 at L = 1 (h_{-1} = 0); homogeneity in g; a brute-force
+ * loop on a tiny case.  One thread per channel, so the sum over b and t is
+ * in a fixed order. */
+int oracle_dA_scale(int64_t Bsz, int64_t L, int64_t D, int64_t N,
+                    const float* u, const float* delta, const float* A,
+                    const float* Bm, const float* Cm, const float* g,
+                    double* scale) {
+  if (Bsz < 0 || L < 0 || D < 0 || N <= 0 || N > 64) return -1;
+  int fail = 0;
+#pragma omp parallel
+  {
+    double* hs = (double*)malloc(sizeof(double) * (size_t)((L + 1) * N));
+    const int ok = hs != NULL;
+    if (!ok) {
+#pragma omp atomic write
+      fail = 1;
+    }
+#pragma omp for schedule(static)
+    for (int64_t d = 0; d < D; ++d) {
+      if (!ok) continue;
+      double s[64];
+      for (int64_t n = 0; n < N; ++n) s[n] = 0.0;
+      for (int64_t b = 0; b < Bsz; ++b) {
+        for (int64_t n = 0; n < N; ++n) hs[n] = 0.0;
+        for (int64_t t = 0; t < L; ++t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], x = u[xi];
+          for (int64_t n = 0; n < N; ++n) {
+            const double e = exp(dt * (double)A[d * N + n]);
+            hs[(t + 1) * N + n] = e * hs[t * N + n] + dt * (double)Bm[bi + n] * x;
+          }
+        }
+        double lam[64];
+        for (int64_t n = 0; n < N; ++n) lam[n] = 0.0;
+        for (int64_t t = L - 1; t >= 0; --t) {
+          const int64_t xi = (b * L + t) * D + d;
+          const int64_t bi = (b * L + t) * N;
+          const double dt = delta[xi], gy = g[xi];
+          for (int64_t n = 0; n < N; ++n) {
+            const double e = exp(dt * (double)A[d * N + n]);
+            lam[n] += (double)Cm[bi + n] * gy;
+            s[n] += fabs(lam[n] * dt * e * hs[t * N + n]);
+            lam[n] *= e;
+          }
+        }
+      }
+      for (int64_t n = 0; n < N; ++n) scale[d * N + n] = s[n];
+    }
+    free(hs);
+  }
+  return fail ? -2 : 0;
+}
+
 /* Forward, VJP and the ddelta scale in one pass per (b, d) pair, for the
  * parity checks at full size: the same expressions, in the same order, as
  * oracle_scan_fwd, oracle_scan_vjp and oracle_ddelta_scale, so the results

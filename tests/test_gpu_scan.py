@@ -114,6 +114,49 @@ def test_parity_shapes_and_chunkings(cuda, shape, chunk_len):
     check_all(scan_inputs.make(*shape, seed=3, a_mode="random"), cuda, chunk_len=chunk_len)
 
 
+def test_dA_at_slow_decays_within_the_reference_precision(cuda):
+    """dA where the decays are slow (random A = -exp(N(0,1)), so |A| delta
+    reaches ~1e-4 and states and adjoints build up over hundreds of steps)
+    at B=4, L=1000, D=3072: dA[d,n] sums 4000 terms lam delta e h that cancel
+    to as little as 1e-5 of their magnitudes S (oracle_dA_scale).  No float32
+    evaluation reaches the plain bar there: the reference's own sequential
+    algorithm run in float32 (torch_ref.scan_sequential on the CPU, gradients
+    by autograd) misses it on a few elements, with worst error ~55 * 2^-24 * S.
+    The bound for dA is the plain bar plus 32 * 2^-24 * S for the default
+    (chunked) call, as for ddelta, and, for the one-chunk call of the
+    sequential mode (a single 1000-step recurrence per state, forward and
+    backward, like the reference's own loop), the larger of that and 4 x the
+    float32 reference algorithm's worst ratio on the same inputs."""
+    from oracle import torch_ref
+    print("case: dA at slow decays B=4 L=1000 D=3072 N=16", flush=True)
+    inputs = scan_inputs.make(4, 1000, 3072, 16, seed=20, a_mode="random")
+    npi = [t.float().numpy() for t in inputs]
+    dA_ref = ref_lib.scan_vjp(*npi)[2]
+    S = ref_lib.dA_scale(*npi[:5], npi[6])
+    eps = 2.0 ** -24
+
+    def ratio(got):
+        err = np.abs(np.asarray(got, dtype=np.float64) - dA_ref)
+        plain = int(np.sum(err > ATOL + RTOL * np.abs(dA_ref)))
+        return float(np.max(err / (eps * S))), plain
+
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    leaves = [t.clone().requires_grad_(True) for t in inputs[:6]]
+    y32 = torch_ref.scan_sequential(*leaves)
+    dA32 = torch.autograd.grad(y32, leaves[2], inputs[6])[0].double().numpy()
+    del y32, leaves
+    r_ref, n_ref = ratio(dA32)
+    _, grads = run_scan(inputs, cuda)
+    r_def, n_def = ratio(grads[2].cpu().numpy())
+    _, grads = run_scan(inputs, cuda, chunk_len="whole")
+    r_seq, n_seq = ratio(grads[2].cpu().numpy())
+    print(f"worst err / (2^-24 S), plain-bar misses: float32 reference {r_ref:.1f} ({n_ref}), "
+          f"default {r_def:.1f} ({n_def}), one chunk {r_seq:.1f} ({n_seq})", flush=True)
+    assert n_ref > 0          # the plain bar is out of reach of float32 here
+    assert r_def <= 32
+    assert r_seq <= max(32.0, 4 * r_ref)
+
+
 def test_parity_long_sequence_many_chunks(cuda):
     print("case: B=2 L=4096 D=128 auto chunking", flush=True)
     check_all(scan_inputs.make(2, 4096, 128, 16, seed=4), cuda)

@@ -7,6 +7,8 @@ differences (gradcheck).  A dropped term, a wrong sign, an off-by-one in time
 or a transposed operand in the oracle fails at least one of these.
 """
 
+import math
+
 import numpy as np
 import pytest
 import scipy.signal
@@ -340,6 +342,66 @@ def test_ddelta_scale_closed_form_at_zero_delta():
     lam = np.flip(np.cumsum(np.flip(Cm[:, :, None, :].astype(np.float64) * g[..., None], 1), 1), 1)
     expect = np.sum(np.abs(lam) * np.abs(Bm[:, :, None, :].astype(np.float64) * u[..., None]), -1)
     np.testing.assert_allclose(S, expect, rtol=1e-12, atol=1e-14)
+
+
+def test_dA_scale_bounds_dA_and_is_homogeneous():
+    """S[d,n] = sum_{b,t} |lam_t delta_t e_t h_{t-1}| (scan_ref.c
+    oracle_dA_scale): S >= |dA| everywhere, with cancellation on random
+    inputs; S is homogeneous of degree 1 in g and in u, and even in each."""
+    *args, g = _rand(2, 40, 6, 16, seed=33, a_mode="random")
+    u, dl, A, Bm, Cm, Dv, g = _f32(*args, g)
+    S = ref_lib.dA_scale(u, dl, A, Bm, Cm, g)
+    dA = ref_lib.scan_vjp(u, dl, A, Bm, Cm, Dv, g)[2]
+    assert S.shape == dA.shape
+    assert np.all(S >= np.abs(dA) * (1 - 1e-12))
+    assert np.median(S / np.maximum(np.abs(dA), 1e-300)) > 1.0   # cancellation happens
+    np.testing.assert_allclose(ref_lib.dA_scale(u, dl, A, Bm, Cm, 2 * g), 2 * S, rtol=1e-13)
+    np.testing.assert_allclose(ref_lib.dA_scale(-2 * u, dl, A, Bm, Cm, g), 2 * S, rtol=1e-12)
+    np.testing.assert_allclose(ref_lib.dA_scale(u, dl, A, Bm, Cm, -g), S, rtol=1e-13)
+
+
+def test_dA_scale_equals_dA_without_cancellation():
+    """With u, B, C, g > 0 every state h and adjoint lam is positive, so every
+    term lam delta e h of dA is positive and S = dA exactly."""
+    rng = np.random.default_rng(34)
+    bsz, L, D, N = 2, 30, 5, 8
+    u = rng.uniform(0.5, 1.5, (bsz, L, D))
+    dl = rng.uniform(0.01, 0.5, (bsz, L, D))
+    A = -rng.uniform(0.1, 3.0, (D, N))
+    Bm = rng.uniform(0.5, 1.5, (bsz, L, N))
+    Cm = rng.uniform(0.5, 1.5, (bsz, L, N))
+    g = rng.uniform(0.5, 1.5, (bsz, L, D))
+    u, dl, A, Bm, Cm, g, Dv = _f32(u, dl, A, Bm, Cm, g, np.ones(D))
+    S = ref_lib.dA_scale(u, dl, A, Bm, Cm, g)
+    dA = ref_lib.scan_vjp(u, dl, A, Bm, Cm, Dv, g)[2]
+    assert np.all(dA > 0)
+    np.testing.assert_allclose(S, dA, rtol=1e-12)
+
+
+def test_dA_scale_brute_force():
+    """A scalar loop over the definition on a tiny case (h_{-1} = 0, lam_t =
+    C_t g_t + e_{t+1} lam_{t+1}); and S = 0 at L = 1, where h_{-1} = 0 makes
+    every term vanish."""
+    *args, g = _rand(2, 5, 3, 4, seed=35, a_mode="random")
+    u, dl, A, Bm, Cm, Dv, g = _f32(*args, g)
+    bsz, L, D = u.shape
+    N = A.shape[1]
+    expect = np.zeros((D, N))
+    for b in range(bsz):
+        for d in range(D):
+            for n in range(N):
+                a = float(A[d, n])
+                e = [math.exp(float(dl[b, t, d]) * a) for t in range(L)]
+                h = [0.0]
+                for t in range(L):
+                    h.append(e[t] * h[-1] + float(dl[b, t, d]) * float(Bm[b, t, n]) * float(u[b, t, d]))
+                lam = 0.0
+                for t in reversed(range(L)):
+                    lam = float(Cm[b, t, n]) * float(g[b, t, d]) + (e[t + 1] * lam if t + 1 < L else 0.0)
+                    expect[d, n] += abs(lam * float(dl[b, t, d]) * e[t] * h[t])
+    np.testing.assert_allclose(ref_lib.dA_scale(u, dl, A, Bm, Cm, g), expect, rtol=1e-12)
+    one = [x[:, :1] for x in (u, dl)]
+    assert not ref_lib.dA_scale(one[0], one[1], A, Bm[:, :1], Cm[:, :1], g[:, :1]).any()
 
 
 def test_fp32_reference_algorithm_needs_the_ddelta_cancellation_term():
