@@ -342,13 +342,17 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // (stride D * 16 floats) from the block's first channel
   const float4* ckb = own_ptr(reinterpret_cast<const float4*>(bf.ckpt + (bk * gm.nck * gm.D + ch0) * kStatePad));
   const IdxT ck_stride = own_sc(static_cast<IdxT>(gm.D * (kStatePad / 4)));
-  const int ck_lane = cl * 4 + grp;
+  // (a lane of a channel past D reads the block's first channel instead:
+  // its u and dy are staged as 0, so its state enters no sum and no store)
+  const int ck_lane = dvalid ? cl * 4 + grp : grp;
   const uint32_t ck_lane_b = static_cast<uint32_t>(ck_lane) * 16u;
 
-  // state after position p - 1 (checkpoint slot p / 8 - 1), p a multiple of 8
+  // state after position p - 1 (checkpoint slot p / 8 - 1), p a multiple of
+  // 8; p is block-uniform, so the test is a scalar branch and the load needs
+  // no per-lane default
   auto load_ckpt = [&](int32_t p) {
     float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p > 0 && dvalid) h4 = row_elem(ckb, p / kCk - 1, ck_stride, ck_lane, ck_lane_b);
+    if (p > 0) h4 = row_elem(ckb, p / kCk - 1, ck_stride, ck_lane, ck_lane_b);
     return h4;
   };
   // fused: the dt bias of the channel this thread stages / flushes, and its
@@ -372,7 +376,8 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   const int64_t zoff = b * gm.zsb + k * gm.zsk + ch0;
   const float* __restrict__ zin = gate ? own_ptr(bf.z + zoff) : nullptr;
   float* __restrict__ dz_out = gate ? own_ptr(bf.dz + zoff) : nullptr;
-  const float* __restrict__ yraw = gate ? own_ptr(bf.y_raw + (b * gm.ysb + k * gm.ysk + ch0)) : nullptr;
+  // (an SGPR base whether or not there is a gate: only read when there is one)
+  const float* __restrict__ yraw = own_ptr(bf.y_raw + (gate ? b * gm.ysb + k * gm.ysk + ch0 : 0));
   float pz[4] = {0.f, 0.f, 0.f, 0.f}, pyr[4] = {0.f, 0.f, 0.f, 0.f};
   auto stage_gate = [&](float (&gv)[4], const TileRows& rows, int nt) {
     if (gate) {
@@ -416,13 +421,16 @@ scan_bwd_kernel(Geom gm, BwdBufs bf) {
   // this block's dB | dC partials of a tile: the 4 waves' channel sums in
   // sRed[rb], added in a fixed order
   auto flush_red = [&](int rb, int32_t ts, int nt) {
-    float* pbc = pbc_blk + static_cast<IdxT>(ts) * (2 * kStatePad);
     for (int i = tid; i < nt * 2 * kStatePad; i += kThreads) {
       const int tt = i / (2 * kStatePad);
       const int w2 = (i / kStatePad) & 1;
       const int n = i % kStatePad;
-      pbc[i] = (sRed[rb][0][tt][w2][n] + sRed[rb][1][tt][w2][n]) +
-               (sRed[rb][2][tt][w2][n] + sRed[rb][3][tt][w2][n]);
+      const float v = (sRed[rb][0][tt][w2][n] + sRed[rb][1][tt][w2][n]) +
+                      (sRed[rb][2][tt][w2][n] + sRed[rb][3][tt][w2][n]);
+      if constexpr (std::is_same<IdxT, int32_t>::value)  // the block base plus a 32-bit offset
+        *at_bytes(pbc_blk, static_cast<uint32_t>(ts * (2 * kStatePad) + i) * 4u) = v;
+      else
+        pbc_blk[static_cast<IdxT>(ts) * (2 * kStatePad) + i] = v;
     }
   };
 
