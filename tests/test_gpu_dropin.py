@@ -36,15 +36,16 @@ ENTRY_POINTS = ["selective_scan", "selective_scan_sequential", "selective_scan_c
 
 
 @pytest.fixture(scope="module")
-def cfg0():
+def single_block():
+    """One MambaBlock's scan: B=2, L=196, d_inner=1536, N=16, fp32, with its oracle results."""
     inputs = synthetic.make(2, 196, 1536, 16, seed=0)
     return inputs, oracle(inputs), ddelta_scale(inputs)
 
 
 @pytest.mark.parametrize("name", ENTRY_POINTS)
-def test_entry_point_matches_oracle(cuda, cfg0, name):
+def test_entry_point_matches_oracle(cuda, single_block, name):
     print(f"case: {name} at B=2 L=196 D=1536 N=16", flush=True)
-    inputs, (y_ref, g_ref), scale = cfg0
+    inputs, (y_ref, g_ref), scale = single_block
     fn = getattr(mvm, name)
     leaves = [t.to(cuda).requires_grad_(True) for t in inputs[:6]]
     y = fn(*leaves)
@@ -54,8 +55,8 @@ def test_entry_point_matches_oracle(cuda, cfg0, name):
         assert_close(a, b, f"{name} {n}", scale=scale if n == "ddelta" else None)
 
 
-def test_metal_entry_point_is_forward_only(cuda, cfg0):
-    inputs, (y_ref, _), _ = cfg0
+def test_metal_entry_point_is_forward_only(cuda, single_block):
+    inputs, (y_ref, _), _ = single_block
     leaves = [t.to(cuda).requires_grad_(True) for t in inputs[:6]]
     y = mvm.selective_scan_metal(*leaves)
     assert not y.requires_grad
