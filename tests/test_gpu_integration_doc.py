@@ -1,4 +1,5 @@
-"""The ctypes binding printed in INTEGRATION.md runs as written.
+"""The ctypes binding printed in the repository's integration guide (the
+markdown file read below) runs as written.
 
 The python block that starts with ``# hip_scan.py`` is executed (with the
 library name replaced by the in-tree path) and its ``hip_selective_scan``
@@ -15,13 +16,14 @@ import torch
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = "INTEGRATION.md"  # the guide whose binding block is executed
 
 
 def _stub_source():
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    text = open(os.path.join(ROOT, GUIDE)).read()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     src = [b for b in blocks if b.startswith("# hip_scan.py")]
-    assert len(src) == 1, "INTEGRATION.md must hold exactly one hip_scan.py block"
+    assert len(src) == 1, f"{GUIDE} must hold exactly one hip_scan.py block"
     return src[0]
 
 
@@ -35,7 +37,7 @@ def test_stub_matches_package_scan(cuda):
     from mlx_vision_mamba_amd import _lib, selective_scan
     src = _stub_source().replace('ctypes.CDLL("libmvm_scan.so")', f"ctypes.CDLL({_lib.LIB_PATH!r})")
     ns = {}
-    exec(compile(src, "INTEGRATION.md:hip_scan.py", "exec"), ns)
+    exec(compile(src, f"{GUIDE}:hip_scan.py", "exec"), ns)
     g = torch.Generator().manual_seed(7)
     B, L, D, N = 2, 100, 192, 16
     x = torch.randn(B, L, D, generator=g)
