@@ -77,7 +77,7 @@ def test_parameter_names_and_init():
     assert names["dt_proj.weight"].shape == (96, 3)
     assert names["out_proj.weight"].shape == (48, 96)
     torch.testing.assert_close(-torch.exp(blk.A_log[0]), -torch.arange(1, 17, dtype=torch.float32))
-    dt = F.softplus(blk.dt_proj.bias)
+    dt = F.softplus(blk.dt_proj.bias.detach())
     assert float(dt.min()) >= 1e-3 * (1 - 1e-5) and float(dt.max()) <= 1e-1 * (1 + 1e-5)
 
 
